@@ -1,0 +1,271 @@
+"""Benchmark the hot path on one MI355X and print ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A "step" is one launch of a kernel over one batch of synthetic input that is
+already resident in HBM. Every BASELINE configuration is measured; the
+headline ``value`` is configuration 3, the fp16 GEMM 2048x4096x4096 in
+TFLOP/s (BASELINE.json ``metric``). Per step: flush L2 + Infinity Cache,
+record a start event, launch, record an end event (all on the stream the
+kernel runs on); K steps are bracketed by synchronisation. Throughput is the
+algorithmic work (FLOP or minimum bytes) divided by the mean event-timed
+kernel duration, and each figure is priced against the MI355X peak.
+
+Each configuration's output is checked against torch on the same device with
+the reference's gate before it is timed. The CPU baseline is the oracle
+(oracle/ops.py, torch eager in fp32) timed on the host cores on a bounded
+slice of each workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+METRIC = "fp16 GEMM TFLOP/s @2048x4096x4096; RMSNorm/softmax/GEMV HBM GB/s"
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _time_steps(fn, steps: int, warmup: int, flush) -> list[float]:
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    end = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for i in range(steps):
+        flush.flush()
+        start[i].record()
+        fn()
+        end[i].record()
+    torch.cuda.synchronize()
+    return [start[i].elapsed_time(end[i]) for i in range(steps)]
+
+
+def _cpu_time(fn, iters: int) -> float:
+    fn()  # warm caches / thread pool
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        fn()
+    return (time.perf_counter() - t0) / iters
+
+
+def main(argv: list[str] | None = None) -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args(argv)
+    if args.gpus != 1:
+        print(
+            "bench.py measures one GPU: this build has no multi-GPU path (every GPU box here has "
+            "one GPU). Run with --gpus 1.",
+            file=sys.stderr,
+        )
+        return 2
+
+    import numpy as np
+    import torch
+
+    from kernelo_amd.benchmark import metrics
+    from kernelo_amd.benchmark.runner import flush_buffer
+    from kernelo_amd.kernels.fused_linear import fused_linear_gelu, linear_gelu_reference
+    from kernelo_amd.kernels.matmul import matmul
+    from kernelo_amd.kernels.rmsnorm import rmsnorm, rmsnorm_reference
+    from kernelo_amd.kernels.softmax import softmax
+    from kernelo_amd.runtime.env import device_caps, host_cores
+    from kernelo_amd.testing import assert_verified, exact_fp32_matmul
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    caps = device_caps(dev)
+    flush = flush_buffer(dev)
+    steps, warmup = args.steps, args.warmup
+    g = torch.Generator().manual_seed(0)
+    results: dict[str, dict] = {}
+
+    def record(name, fn, work, unit, peak, extra=None):
+        samples = _time_steps(fn, steps, warmup, flush)
+        mean_ms = float(np.mean(samples))
+        med_ms = float(np.median(samples))
+        rate = (work / (mean_ms * 1e-3)) / (1e12 if unit == "TFLOP/s" else 1e9)
+        entry = {
+            "value": rate,
+            "unit": unit,
+            "mean_us": mean_ms * 1e3,
+            "median_us": med_ms * 1e3,
+            "min_us": float(np.min(samples)) * 1e3,
+            "work": work,
+            "roofline": {
+                "bound": "mfma" if unit == "TFLOP/s" else "hbm",
+                "achieved": rate,
+                "peak": peak,
+                "unit": "TFLOP/s" if unit == "TFLOP/s" else "GB/s",
+                "frac": rate / peak,
+                "traffic": None,
+            },
+        }
+        if extra:
+            entry.update(extra)
+        results[name] = entry
+        _log(f"{name}: {rate:.1f} {unit} ({entry['roofline']['frac'] * 100:.1f}% of peak), "
+             f"mean {mean_ms * 1e3:.1f} us")
+        return entry
+
+    hbm = caps.peak_hbm_gbps
+    f16_peak = caps.peak_fp16_tflops
+
+    # --- calibration: a plain device-to-device copy of 1 GiB (read + write) -----
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    copy = record("hbm_copy_1GiB", lambda: dst.copy_(src), 2 * src.numel() * 4, "GB/s", hbm)
+    del src, dst
+
+    # --- config 1: RMSNorm fp32 [4096,4096], eps=1e-6 ----------------------------
+    x = torch.randn(4096, 4096, generator=g)
+    gamma = 1.0 + 0.1 * torch.randn(4096, generator=g)
+    dx, dgamma = x.to(dev), gamma.to(dev)
+    assert_verified(rmsnorm_reference(dx, dgamma, eps=1e-6), rmsnorm(dx, dgamma, eps=1e-6),
+                    context="rmsnorm config 1")
+    record("rmsnorm_fp32_4096x4096", lambda: rmsnorm(dx, dgamma, eps=1e-6),
+           metrics.rmsnorm_bytes(4096, 4096, 4), "GB/s", hbm)
+
+    # --- config 2: softmax fp16 [8192,4096] and [8192,11008], 1% rows +60 ---------
+    for cols in (4096, 11008):
+        s = 3.0 * torch.randn(8192, cols, generator=g)
+        s[torch.randperm(8192, generator=g)[:82]] += 60.0
+        ds = s.to(torch.float16).to(dev)
+        out = softmax(ds)
+        assert torch.isfinite(out).all()
+        assert_verified(torch.softmax(ds.float(), -1), out, dtype=torch.float16,
+                        context=f"softmax config 2 ({cols})")
+        record(f"softmax_fp16_8192x{cols}", lambda ds=ds: softmax(ds),
+               metrics.softmax_bytes(8192, cols, 2), "GB/s", hbm)
+        del ds, s
+
+    # --- config 3: GEMM fp16 2048x4096x4096 (headline) -----------------------------
+    M, N, K = 2048, 4096, 4096
+    a = (torch.randn(M, K, generator=g) / K**0.5).to(torch.float16).to(dev)
+    b = (torch.randn(K, N, generator=g) / K**0.5).to(torch.float16).to(dev)
+    with exact_fp32_matmul():
+        assert_verified(torch.matmul(a.float(), b.float()), matmul(a, b), dtype=torch.float16,
+                        context="gemm config 3")
+    gemm = record("gemm_fp16_2048x4096x4096", lambda: matmul(a, b),
+                  metrics.matmul_flops(M, N, K), "TFLOP/s", f16_peak)
+    torch_gemm = _time_steps(lambda: torch.matmul(a, b), steps, warmup, flush)
+    gemm["torch_hipblaslt_tflops"] = metrics.matmul_flops(M, N, K) / (np.mean(torch_gemm) * 1e-3) / 1e12
+
+    # --- config 4: fused linear fp16 4096x11008x4096 + bias + GELU(tanh) -----------
+    FM, FN, FK = 4096, 11008, 4096
+    fx = (torch.randn(FM, FK, generator=g) / FK**0.5).to(torch.float16).to(dev)
+    fw = (torch.randn(FK, FN, generator=g) / FK**0.5).to(torch.float16).to(dev)
+    fb = (0.02 * torch.randn(FN, generator=g)).to(torch.float16).to(dev)
+    assert_verified(linear_gelu_reference(fx, fw, fb), fused_linear_gelu(fx, fw, fb),
+                    context="fused linear config 4")
+    fused = record("fused_linear_fp16_4096x11008x4096", lambda: fused_linear_gelu(fx, fw, fb),
+                   metrics.matmul_flops(FM, FN, FK), "TFLOP/s", f16_peak)
+    unfused = _time_steps(lambda: linear_gelu_reference(fx, fw, fb), steps, warmup, flush)
+    fused["unfused_torch_3op_us"] = float(np.mean(unfused)) * 1e3
+    fused["speedup_vs_unfused"] = float(np.mean(unfused)) * 1e3 / fused["mean_us"]
+    del fx, fw
+
+    # --- config 5a: decode GEMV bf16 1x11008x4096 ----------------------------------
+    vx = (torch.rand(1, 4096, generator=g) * 2 - 1).to(torch.bfloat16).to(dev)
+    vw = (torch.rand(4096, 11008, generator=g) * 2 - 1).to(torch.bfloat16).to(dev)
+    assert_verified(torch.matmul(vx.float(), vw.float()), matmul(vx, vw), dtype=torch.bfloat16,
+                    context="gemv config 5a")
+    record("gemv_bf16_1x11008x4096", lambda: matmul(vx, vw),
+           metrics.matmul_bytes(1, 11008, 4096, 2), "GB/s", hbm)
+
+    # --- CPU baseline: the oracle on the host cores, bounded slices ----------------
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import ops
+
+        cores = host_cores()
+        torch.set_num_threads(cores)
+        rows = 256
+        ca, cb = a[:rows].cpu(), b.cpu()
+        secs = _cpu_time(lambda: ops.matmul_ref(ca, cb), 3)
+        cpu = {
+            "value": metrics.matmul_flops(rows, N, K) / secs / 1e12,
+            "unit": "TFLOP/s",
+            "cores": cores,
+            "kind": "port",
+            "sample": f"oracle matmul_ref (torch fp32 on CPU) on A[:{rows}] @ B, "
+                      f"{rows}x{N}x{K}, mean of 3 after 1 warmup",
+        }
+        results["gemm_fp16_2048x4096x4096"]["cpu_baseline"] = cpu
+        secs = _cpu_time(lambda: ops.rmsnorm_ref(x, gamma, 1e-6), 5)
+        results["rmsnorm_fp32_4096x4096"]["cpu_baseline"] = {
+            "value": metrics.rmsnorm_bytes(4096, 4096, 4) / secs / 1e9, "unit": "GB/s",
+            "cores": cores, "kind": "port", "sample": "oracle rmsnorm_ref, full [4096,4096]",
+        }
+        cs = (3.0 * torch.randn(1024, 4096, generator=g)).to(torch.float16)
+        secs = _cpu_time(lambda: ops.softmax_ref(cs), 5)
+        results["softmax_fp16_8192x4096"]["cpu_baseline"] = {
+            "value": metrics.softmax_bytes(1024, 4096, 2) / secs / 1e9, "unit": "GB/s",
+            "cores": cores, "kind": "port", "sample": "oracle softmax_ref on [1024,4096] fp16",
+        }
+        cvx, cvw = vx.cpu(), vw.cpu()
+        secs = _cpu_time(lambda: ops.matmul_ref(cvx, cvw), 3)
+        results["gemv_bf16_1x11008x4096"]["cpu_baseline"] = {
+            "value": metrics.matmul_bytes(1, 11008, 4096, 2) / secs / 1e9, "unit": "GB/s",
+            "cores": cores, "kind": "port", "sample": "oracle matmul_ref, full 1x11008x4096 bf16",
+        }
+        fxs, fws, fbs = (torch.randn(64, FK, generator=g) / 64).to(torch.float16), \
+            (torch.randn(FK, FN, generator=g) / 64).to(torch.float16), fb.cpu()
+        secs = _cpu_time(lambda: ops.linear_gelu_ref(fxs, fws, fbs), 2)
+        results["fused_linear_fp16_4096x11008x4096"]["cpu_baseline"] = {
+            "value": metrics.matmul_flops(64, FN, FK) / secs / 1e12, "unit": "TFLOP/s",
+            "cores": cores, "kind": "port",
+            "sample": f"oracle linear_gelu_ref on X[:64], 64x{FN}x{FK}",
+        }
+
+    line = {
+        "metric": METRIC,
+        "value": gemm["value"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": gemm["mean_us"] / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {
+            "workload": "gemm_fp16_2048x4096x4096",
+            "M": M,
+            "N": N,
+            "K": K,
+            "device": caps.name,
+            "arch": caps.gcn_arch,
+            "flush_bytes": caps.flush_bytes,
+        },
+        "roofline": gemm["roofline"],
+        "cpu_baseline": cpu,
+        "configs": results,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,143 @@
+/*
+ * kernelo_amd C-ABI: the drop-in device boundary for KernelForge's tunable
+ * kernel set, rebuilt as hand-written HIP kernels for gfx950 (MI355X).
+ *
+ * In the reference every kernel is launched from Python with raw pointers,
+ * dimensions, strides and compile-time tile parameters:
+ *   matmul_kernel[grid](a, b, c, M, N, K, strides..., BLOCK_*, GROUP_M,
+ *                       num_warps, num_stages)   kernelforge/kernels/matmul.py:132-155
+ *   fused_linear_gelu_kernel[grid](...)           kernelforge/kernels/fused_linear.py:112-157
+ *   softmax_kernel[grid](...)                     kernelforge/kernels/softmax.py:70-104
+ *   rmsnorm_kernel[grid](...)                     kernelforge/kernels/rmsnorm.py:81-127
+ *   rmsnorm_forward_cuda(x, gamma, eps)           kernelforge/csrc/rmsnorm.cu:19-57
+ * These entry points take exactly that information, plus the HIP stream the
+ * launch is enqueued on (torch's current stream; the reference launches on
+ * the current CUDA stream, csrc/rmsnorm.cu:41).
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers; strides are in elements, not bytes.
+ *   - Nothing is allocated or freed; outputs are caller-owned.
+ *   - Launches are asynchronous on `stream`; nothing synchronises.
+ *   - A zero-sized problem returns KF_OK without launching
+ *     (csrc/rmsnorm.cu:27-29).
+ *   - The return value is KF_OK or a negative KF_ERR_* code; the message for
+ *     the last failure on the calling thread is kf_last_error().
+ */
+#ifndef KERNELO_AMD_H_
+#define KERNELO_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types. Double is refused, as in csrc/rmsnorm.cpp:23-30. */
+enum {
+  KF_DTYPE_F32 = 0,
+  KF_DTYPE_F16 = 1,
+  KF_DTYPE_BF16 = 2
+};
+
+/* Status codes. The Python loader maps them onto exception classes whose
+ * names drive the tuner's failure classification (kernelforge/tuning/tuner.py:60-71). */
+enum {
+  KF_OK = 0,
+  KF_ERR_INVALID_ARGUMENT = -1, /* bad shape, stride, pointer or parameter   */
+  KF_ERR_NOT_BUILT = -2,        /* no instantiation for this tile config      */
+  KF_ERR_OUT_OF_RESOURCES = -3, /* config exceeds LDS / register / block caps */
+  KF_ERR_LAUNCH = -4,           /* the HIP runtime rejected the launch        */
+  KF_ERR_UNSUPPORTED_DTYPE = -5,
+  KF_ERR_WORKSPACE = -6,        /* caller workspace missing or too small      */
+  KF_ERR_OUT_OF_MEMORY = -7     /* hipErrorOutOfMemory from the runtime       */
+};
+
+/* GEMM epilogues. */
+enum {
+  KF_EPILOGUE_NONE = 0,      /* C = A @ B                                     */
+  KF_EPILOGUE_BIAS_GELU = 1  /* C = gelu_tanh(A @ B + bias), fused_linear.py:94-104 */
+};
+
+/* Library identification: ABI version and the offload target it was built for. */
+int kf_abi_version(void);
+const char* kf_build_target(void);
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* kf_last_error(void);
+
+/*
+ * Tiled MFMA GEMM, optionally with the fused bias + tanh-GELU epilogue.
+ * Replaces matmul() (kernels/matmul.py:132-155) and fused_linear_gelu()
+ * (kernels/fused_linear.py:112-157).
+ *
+ *   C[M,N] = A[M,K] @ B[K,N]                    (epilogue KF_EPILOGUE_NONE)
+ *   C[M,N] = gelu_tanh(A @ B + bias[N])         (epilogue KF_EPILOGUE_BIAS_GELU)
+ *
+ * fp32 accumulation; C is written in the input dtype. Any strides are
+ * accepted (e.g. nn.Linear weight.t()), as in the reference; 16-byte vector
+ * loads are used where pointers and strides allow them, scalar loads
+ * otherwise. Tile parameters select one ahead-of-time instantiation:
+ *   block_m, block_n, block_k : macro tile
+ *   waves                     : wavefronts (64 lanes) per workgroup
+ *   stages                    : LDS buffers (2 = double buffered)
+ *   group_m                   : rows of tiles per launch-order group
+ * Returns KF_ERR_NOT_BUILT for a tile config that was not instantiated.
+ */
+int kf_gemm(int dtype, const void* A, const void* B, const void* bias, void* C,
+            int64_t M, int64_t N, int64_t K,
+            int64_t lda_m, int64_t lda_k, int64_t ldb_k, int64_t ldb_n,
+            int64_t ldc_m, int64_t ldc_n, int epilogue,
+            int block_m, int block_n, int block_k, int waves, int stages, int group_m,
+            void* stream);
+
+/* 1 if (dtype, tile config) has an instantiation in this build, else 0. */
+int kf_gemm_has_variant(int dtype, int block_m, int block_n, int block_k, int waves, int stages);
+
+/* Number of GEMM instantiations, and the tile config of instantiation `index`
+ * (for the search space's "was it built" rule). Returns KF_OK or an error. */
+int kf_gemm_variant_count(void);
+int kf_gemm_variant_info(int index, int* dtype, int* block_m, int* block_n, int* block_k,
+                         int* waves, int* stages);
+
+/*
+ * Split-K GEMV for decode shapes: y[M,N] = x[M,K] @ W[K,N], M <= 8.
+ * The reference runs decode through the same matmul at M=1
+ * (kernels/matmul.py:132-155, tuning/search.py:377-386); this is its
+ * HBM-bound replacement. Partial sums over `split_k` slices of K are reduced
+ * deterministically (fixed order) by the last workgroup of each column
+ * block, using a caller-provided workspace of kf_gemv_workspace_bytes()
+ * bytes whose counter region must be zero before the first call (the
+ * kernel leaves it zero again). epilogue as for kf_gemm.
+ */
+int kf_gemv(int dtype, const void* x, const void* W, const void* bias, void* y,
+            int64_t M, int64_t N, int64_t K,
+            int64_t ldx_m, int64_t ldx_k, int64_t ldw_k, int64_t ldw_n,
+            int64_t ldy_m, int64_t ldy_n, int epilogue,
+            int split_k, int waves, void* workspace, size_t workspace_bytes, void* stream);
+size_t kf_gemv_workspace_bytes(int64_t M, int64_t N, int split_k);
+
+/*
+ * Single-pass row softmax over the last dimension, fp32 internal.
+ * Replaces softmax() (kernels/softmax.py:70-104). Rows must have unit column
+ * stride. block_size (a power of two >= cols) / (waves*64) is the number of
+ * elements each lane holds; rows_per_program rows are handled per workgroup.
+ */
+int kf_softmax(int dtype, const void* x, void* y, int64_t rows, int64_t cols,
+               int64_t x_row_stride, int64_t y_row_stride,
+               int block_size, int rows_per_program, int waves, void* stream);
+
+/*
+ * Single-pass RMSNorm: y = x * rsqrt(mean(x^2) + eps) * gamma, fp32 math.
+ * Replaces rmsnorm() (kernels/rmsnorm.py:81-127) and rmsnorm_forward_cuda()
+ * (csrc/rmsnorm.cu:19-57). Same tile parameters as kf_softmax.
+ */
+int kf_rmsnorm(int dtype, const void* x, const void* gamma, void* y, int64_t rows,
+               int64_t cols, int64_t x_row_stride, int64_t y_row_stride, float eps,
+               int block_size, int rows_per_program, int waves, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KERNELO_AMD_H_ */

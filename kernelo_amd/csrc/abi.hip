@@ -1,0 +1,36 @@
+// Library-wide C-ABI pieces: error reporting and build identification.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "common.h"
+
+namespace kf {
+
+namespace {
+thread_local char g_last_error[512] = "";
+}
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+}
+
+int launch_status(const char* what) {
+  const hipError_t err = hipGetLastError();
+  if (err == hipSuccess) return KF_OK;
+  set_error("%s: launch failed: %s (%s)", what, hipGetErrorName(err), hipGetErrorString(err));
+  if (err == hipErrorOutOfMemory) return KF_ERR_OUT_OF_MEMORY;
+  if (err == hipErrorLaunchOutOfResources || err == hipErrorInvalidConfiguration)
+    return KF_ERR_OUT_OF_RESOURCES;
+  return KF_ERR_LAUNCH;
+}
+
+}  // namespace kf
+
+extern "C" int kf_abi_version(void) { return 1; }
+
+extern "C" const char* kf_build_target(void) { return "gfx950"; }
+
+extern "C" const char* kf_last_error(void) { return kf::g_last_error; }

@@ -1,0 +1,30 @@
+// Registry entry for one compiled GEMM tile configuration.
+#pragma once
+
+#include <stdint.h>
+
+namespace kf {
+namespace gemm {
+
+// Kernel argument block (passed by value).
+struct Args {
+  const void* A;
+  const void* B;
+  const void* bias;
+  void* C;
+  int64_t M, N, K;
+  int64_t lda_m, lda_k, ldb_k, ldb_n, ldc_m, ldc_n;
+  int epilogue;
+  int group_m;
+};
+
+struct Entry {
+  int bm, bn, bk, waves, stages;
+  int lds_bytes;
+  const void* kernel;  // __global__ gemm_kernel<...> for this tile and loader pair
+};
+
+using TableFn = const Entry* (*)(int*);
+
+}  // namespace gemm
+}  // namespace kf

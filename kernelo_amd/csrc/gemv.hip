@@ -1,0 +1,265 @@
+// Split-K GEMV for decode-shaped products, y[M,N] = x[M,K] @ W[K,N], M <= 8.
+//
+// HBM-bound: every byte of W is read exactly once. A workgroup owns a strip of
+// 64*V columns (one 16-byte vector per lane, V = 16/sizeof(T)) and one of
+// `split_k` slices of K; its waves stride through the slice's rows so each
+// wave issues fully coalesced 1 KiB row segments. Waves are combined through
+// LDS, slices through an fp32 workspace: the last workgroup to finish a
+// column strip (atomic ticket) sums the slices in fixed order, so results
+// are bitwise reproducible run to run.
+//
+// The reference has no GEMV: decode runs through matmul_kernel with
+// BLOCK_M=16 (kernels/matmul.py:54-113, tuning/search.py:377-386).
+#include <math.h>
+
+#include "common.h"
+
+namespace kf {
+
+namespace {
+
+constexpr int kGemvMaxWaves = 16;
+constexpr int kGemvUnroll = 8;        // rows of W in flight per lane
+constexpr size_t kGemvMaxLds = 64 * 1024;  // dynamic LDS without an opt-in attribute
+constexpr float kGeluC = 1.5957691216057308f;  // 2*sqrt(2/pi)
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float gelu_tanh(float a) {
+  // gelu(a) = 0.5a(1+tanh(sqrt(2/pi)(a+0.044715a^3))) = a / (1 + exp(-2sqrt(2/pi)(...)))
+  const float inner = kGeluC * (a + 0.044715f * a * a * a);
+  return a / (1.0f + __builtin_amdgcn_exp2f(-inner * kLog2e));
+}
+
+template <typename T, int MR>
+__global__ __launch_bounds__(1024) void gemv_splitk(
+    const T* __restrict__ x, const T* __restrict__ W, const T* __restrict__ bias,
+    T* __restrict__ y, int64_t M, int64_t N, int64_t K, int64_t ldx_m, int64_t ldx_k,
+    int64_t ldw_k, int64_t ldw_n, int64_t ldy_m, int64_t ldy_n, int epilogue, int split_k,
+    int vec, float* __restrict__ ws, unsigned* __restrict__ tickets) {
+  constexpr int V = Vec<T>::N;
+  constexpr int BN = kWave * V;
+  // red[wave][m][column]: nwaves*MR*BN floats of dynamic LDS.
+  extern __shared__ float red[];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int nwaves = blockDim.x / kWave;
+  const int64_t nb = blockIdx.x;
+  const int64_t col0 = nb * BN + static_cast<int64_t>(lane) * V;
+  const int s = blockIdx.y;
+  const int64_t kc = ceil_div(K, split_k);
+  const int64_t kbeg = static_cast<int64_t>(s) * kc;
+  const int64_t kend = (kbeg + kc < K) ? kbeg + kc : K;
+  const bool full = vec && (col0 + V <= N);
+
+  float acc[MR][V];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int e = 0; e < V; ++e) acc[m][e] = 0.f;
+
+  auto load_w = [&](int64_t k, float (&w)[V]) {
+    const T* row = W + k * ldw_k;
+    if (full) {
+      T tmp[V];
+      load16(row + col0, tmp);
+#pragma unroll
+      for (int e = 0; e < V; ++e) w[e] = to_f32(tmp[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) w[e] = (col0 + e < N) ? to_f32(row[(col0 + e) * ldw_n]) : 0.f;
+    }
+  };
+
+  int64_t k = kbeg + wave;
+  // Main loop: kGemvUnroll rows per wave per trip, all loads issued first.
+  for (; k + static_cast<int64_t>(kGemvUnroll - 1) * nwaves < kend;
+       k += static_cast<int64_t>(kGemvUnroll) * nwaves) {
+    float w[kGemvUnroll][V];
+#pragma unroll
+    for (int u = 0; u < kGemvUnroll; ++u) load_w(k + static_cast<int64_t>(u) * nwaves, w[u]);
+#pragma unroll
+    for (int u = 0; u < kGemvUnroll; ++u) {
+      const int64_t kk = k + static_cast<int64_t>(u) * nwaves;
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const float xv = (m < M) ? to_f32(x[m * ldx_m + kk * ldx_k]) : 0.f;
+#pragma unroll
+        for (int e = 0; e < V; ++e) acc[m][e] = __builtin_fmaf(xv, w[u][e], acc[m][e]);
+      }
+    }
+  }
+  for (; k < kend; k += nwaves) {
+    float w[V];
+    load_w(k, w);
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const float xv = (m < M) ? to_f32(x[m * ldx_m + k * ldx_k]) : 0.f;
+#pragma unroll
+      for (int e = 0; e < V; ++e) acc[m][e] = __builtin_fmaf(xv, w[e], acc[m][e]);
+    }
+  }
+
+  // Combine waves in fixed order through LDS.
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int e = 0; e < V; ++e) red[(wave * MR + m) * BN + lane * V + e] = acc[m][e];
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      float r = red[m * BN + lane * V + e];
+      for (int w = 1; w < nwaves; ++w) r += red[(w * MR + m) * BN + lane * V + e];
+      acc[m][e] = r;
+    }
+
+  if (split_k > 1) {
+    // Publish this slice's partial sums, then take a ticket for the strip.
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      if (m >= M) break;
+      float* dst = ws + (static_cast<int64_t>(s) * M + m) * N;
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        if (col0 + e < N) dst[col0 + e] = acc[m][e];
+    }
+    __threadfence();
+    unsigned ticket = 0;
+    if (lane == 0) ticket = atomicAdd(&tickets[nb], 1u);
+    ticket = __shfl(ticket, 0, kWave);
+    if (ticket != static_cast<unsigned>(split_k - 1)) return;
+    __threadfence();
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      if (m >= M) break;
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        float r = 0.f;
+        if (col0 + e < N)
+          for (int q = 0; q < split_k; ++q) r += ws[(static_cast<int64_t>(q) * M + m) * N + col0 + e];
+        acc[m][e] = r;
+      }
+    }
+    if (lane == 0) tickets[nb] = 0u;  // ready for the next launch
+  }
+
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    if (m >= M) break;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const int64_t c = col0 + e;
+      if (c >= N) continue;
+      float v = acc[m][e];
+      if (epilogue == KF_EPILOGUE_BIAS_GELU) v = gelu_tanh(v + to_f32(bias[c]));
+      y[m * ldy_m + c * ldy_n] = from_f32<T>(v);
+    }
+  }
+}
+
+size_t ticket_bytes(int64_t N) {
+  // One ticket per 64-column strip covers every dtype (strips are >= 64 wide).
+  return static_cast<size_t>((ceil_div(N, 64) * 4 + 255) / 256 * 256);
+}
+
+template <typename T>
+int launch_gemv(const void* x, const void* W, const void* bias, void* y, int64_t M, int64_t N,
+                int64_t K, int64_t ldx_m, int64_t ldx_k, int64_t ldw_k, int64_t ldw_n,
+                int64_t ldy_m, int64_t ldy_n, int epilogue, int split_k, int waves, void* ws,
+                hipStream_t s) {
+  constexpr int V = Vec<T>::N;
+  const bool vec = ldw_n == 1 && aligned16(W) && (ldw_k * sizeof(T)) % 16 == 0;
+  const dim3 grid(static_cast<unsigned>(ceil_div(N, kWave * V)), static_cast<unsigned>(split_k));
+  const dim3 block(waves * kWave);
+  unsigned* tickets = static_cast<unsigned*>(ws);
+  float* partial = ws ? reinterpret_cast<float*>(static_cast<char*>(ws) + ticket_bytes(N)) : nullptr;
+  auto go = [&](auto mr) -> int {
+    constexpr int MR = decltype(mr)::value;
+    const size_t lds = static_cast<size_t>(waves) * MR * kWave * V * sizeof(float);
+    if (lds > kGemvMaxLds) {
+      set_error("gemv: waves=%d x %d rows needs %zu B of LDS for the wave reduction (limit %zu)",
+                waves, MR, lds, kGemvMaxLds);
+      return KF_ERR_OUT_OF_RESOURCES;
+    }
+    hipLaunchKernelGGL((gemv_splitk<T, MR>), grid, block, lds, s, static_cast<const T*>(x),
+                       static_cast<const T*>(W), static_cast<const T*>(bias), static_cast<T*>(y),
+                       M, N, K, ldx_m, ldx_k, ldw_k, ldw_n, ldy_m, ldy_n, epilogue, split_k,
+                       vec ? 1 : 0, partial, tickets);
+    return launch_status("gemv");
+  };
+  if (M <= 1) return go(std::integral_constant<int, 1>{});
+  if (M <= 2) return go(std::integral_constant<int, 2>{});
+  if (M <= 4) return go(std::integral_constant<int, 4>{});
+  return go(std::integral_constant<int, 8>{});
+}
+
+}  // namespace
+}  // namespace kf
+
+extern "C" size_t kf_gemv_workspace_bytes(int64_t M, int64_t N, int split_k) {
+  if (M <= 0 || N <= 0 || split_k <= 1) return 0;
+  return kf::ticket_bytes(N) + static_cast<size_t>(split_k) * M * N * sizeof(float);
+}
+
+extern "C" int kf_gemv(int dtype, const void* x, const void* W, const void* bias, void* y,
+                       int64_t M, int64_t N, int64_t K, int64_t ldx_m, int64_t ldx_k,
+                       int64_t ldw_k, int64_t ldw_n, int64_t ldy_m, int64_t ldy_n, int epilogue,
+                       int split_k, int waves, void* workspace, size_t workspace_bytes,
+                       void* stream) {
+  using namespace kf;
+  if (M < 0 || N < 0 || K < 0) {
+    set_error("gemv: negative shape");
+    return KF_ERR_INVALID_ARGUMENT;
+  }
+  if (M > 8) {
+    set_error("gemv: M=%lld exceeds the decode limit of 8 rows", (long long)M);
+    return KF_ERR_INVALID_ARGUMENT;
+  }
+  if (epilogue != KF_EPILOGUE_NONE && epilogue != KF_EPILOGUE_BIAS_GELU) {
+    set_error("gemv: unknown epilogue %d", epilogue);
+    return KF_ERR_INVALID_ARGUMENT;
+  }
+  if (waves < 1 || waves > kGemvMaxWaves) {
+    set_error("gemv: waves=%d outside 1..%d", waves, kGemvMaxWaves);
+    return KF_ERR_OUT_OF_RESOURCES;
+  }
+  if (split_k < 1 || split_k > 65535) {
+    set_error("gemv: split_k=%d outside 1..65535", split_k);
+    return KF_ERR_INVALID_ARGUMENT;
+  }
+  if (M == 0 || N == 0) return KF_OK;
+  if (!x && K > 0) {
+    set_error("gemv: null x");
+    return KF_ERR_INVALID_ARGUMENT;
+  }
+  if ((!W && K > 0) || !y || (epilogue == KF_EPILOGUE_BIAS_GELU && !bias)) {
+    set_error("gemv: null pointer");
+    return KF_ERR_INVALID_ARGUMENT;
+  }
+  if (split_k > 1) {
+    const size_t need = kf_gemv_workspace_bytes(M, N, split_k);
+    if (!workspace || workspace_bytes < need || !aligned16(workspace)) {
+      set_error("gemv: split_k=%d needs a 16-byte aligned workspace of %zu bytes, got %zu",
+                split_k, need, workspace ? workspace_bytes : (size_t)0);
+      return KF_ERR_WORKSPACE;
+    }
+  }
+  auto s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case KF_DTYPE_F32:
+      return launch_gemv<float>(x, W, bias, y, M, N, K, ldx_m, ldx_k, ldw_k, ldw_n, ldy_m, ldy_n,
+                                epilogue, split_k, waves, workspace, s);
+    case KF_DTYPE_F16:
+      return launch_gemv<f16>(x, W, bias, y, M, N, K, ldx_m, ldx_k, ldw_k, ldw_n, ldy_m, ldy_n,
+                              epilogue, split_k, waves, workspace, s);
+    case KF_DTYPE_BF16:
+      return launch_gemv<bf16>(x, W, bias, y, M, N, K, ldx_m, ldx_k, ldw_k, ldw_n, ldy_m, ldy_n,
+                               epilogue, split_k, waves, workspace, s);
+    default:
+      set_error("gemv: unsupported dtype code %d", dtype);
+      return KF_ERR_UNSUPPORTED_DTYPE;
+  }
+}

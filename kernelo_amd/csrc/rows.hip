@@ -1,0 +1,302 @@
+// Single-pass row kernels for gfx950: softmax and RMSNorm.
+//
+// One workgroup owns `rows_per_program` whole rows; each row is read from HBM
+// exactly once into registers (16-byte loads, EPT fp32 values per lane),
+// reduced with wave64 shuffles plus one LDS exchange across waves, and
+// written once. These are the HBM-bound counterparts of the reference's
+// softmax_kernel (kernels/softmax.py:31-58) and rmsnorm_kernel
+// (kernels/rmsnorm.py:41-72).
+#include <math.h>
+
+#include "common.h"
+
+namespace kf {
+
+namespace {
+
+constexpr int kMaxWaves = 16;  // 1024 lanes, the workgroup limit
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Lane `t` of a `nt`-lane workgroup owns vector slots t, t+nt, t+2nt, ... of
+// the row; slot s covers columns [s*V, s*V+V). `vec` says whether the row is
+// 16-byte aligned, so a full slot can be one load.
+template <typename T, int EPT>
+struct RowTile {
+  static constexpr int V = (EPT < Vec<T>::N) ? EPT : Vec<T>::N;
+  static constexpr int NV = EPT / V;
+  float v[EPT];
+
+  __device__ __forceinline__ void load(const T* row, int64_t cols, int t, int nt, bool vec,
+                                       float fill) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t c0 = (static_cast<int64_t>(j) * nt + t) * V;
+      if (vec && V == Vec<T>::N && c0 + V <= cols) {
+        T tmp[Vec<T>::N];
+        load16(row + c0, tmp);
+#pragma unroll
+        for (int e = 0; e < V; ++e) v[j * V + e] = to_f32(tmp[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < V; ++e) v[j * V + e] = (c0 + e < cols) ? to_f32(row[c0 + e]) : fill;
+      }
+    }
+  }
+
+  template <typename F>
+  __device__ __forceinline__ void store(T* row, int64_t cols, int t, int nt, bool vec, F f) const {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t c0 = (static_cast<int64_t>(j) * nt + t) * V;
+      if (vec && V == Vec<T>::N && c0 + V <= cols) {
+        T tmp[Vec<T>::N];
+#pragma unroll
+        for (int e = 0; e < V; ++e) tmp[e] = from_f32<T>(f(v[j * V + e], j * V + e));
+        store16(row + c0, tmp);
+      } else {
+#pragma unroll
+        for (int e = 0; e < V; ++e)
+          if (c0 + e < cols) row[c0 + e] = from_f32<T>(f(v[j * V + e], j * V + e));
+      }
+    }
+  }
+};
+
+// Workgroup reduction: wave64 butterfly, then one LDS exchange. `slot`
+// alternates between two buffers so a reduction needs a single barrier: the
+// buffer reused two reductions later cannot be overwritten before every wave
+// has passed the barrier of the reduction in between.
+template <bool IsMax>
+__device__ __forceinline__ float block_reduce(float x, float (*part)[kMaxWaves], int& slot,
+                                              int nwaves) {
+  x = IsMax ? wave_max(x) : wave_sum(x);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  if (nwaves == 1) return x;
+  if (lane == 0) part[slot][wave] = x;
+  __syncthreads();
+  float r = part[slot][0];
+  for (int w = 1; w < nwaves; ++w) r = IsMax ? fmaxf(r, part[slot][w]) : r + part[slot][w];
+  slot ^= 1;
+  return r;
+}
+
+template <typename T, int EPT>
+__global__ __launch_bounds__(1024) void softmax_rows(const T* __restrict__ x, T* __restrict__ y,
+                                                     int64_t xrs, int64_t yrs, int64_t rows,
+                                                     int64_t cols, int rpp, int vec) {
+  __shared__ float part[2][kMaxWaves];
+  int slot = 0;
+  const int t = threadIdx.x;
+  const int nt = blockDim.x;
+  const int nwaves = nt / kWave;
+  for (int i = 0; i < rpp; ++i) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * rpp + i;
+    if (r >= rows) break;
+    RowTile<T, EPT> tile;
+    // Out-of-row lanes hold -inf: they lose the max and add exp(-inf)=0.
+    tile.load(x + r * xrs, cols, t, nt, vec, -INFINITY);
+    float m = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) m = fmaxf(m, tile.v[e]);
+    m = block_reduce<true>(m, part, slot, nwaves);
+    // exp(x - m) = exp2((x - m) * log2(e)); v_exp_f32 is the hardware exp2.
+    const float ms = m * kLog2e;
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      tile.v[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(tile.v[e], kLog2e, -ms));
+      s += tile.v[e];
+    }
+    s = block_reduce<false>(s, part, slot, nwaves);
+    const float inv = 1.0f / s;
+    tile.store(y + r * yrs, cols, t, nt, vec, [inv](float v, int) { return v * inv; });
+  }
+}
+
+template <typename T, int EPT>
+__global__ __launch_bounds__(1024) void rmsnorm_rows(const T* __restrict__ x,
+                                                     const T* __restrict__ gamma,
+                                                     T* __restrict__ y, int64_t xrs, int64_t yrs,
+                                                     int64_t rows, int64_t cols, float eps,
+                                                     int rpp, int vec) {
+  __shared__ float part[2][kMaxWaves];
+  int slot = 0;
+  const int t = threadIdx.x;
+  const int nt = blockDim.x;
+  const int nwaves = nt / kWave;
+  // gamma is shared by all rows of the program: read it once.
+  RowTile<T, EPT> g;
+  g.load(gamma, cols, t, nt, vec, 0.f);
+  const float inv_cols = 1.0f / static_cast<float>(cols);
+  for (int i = 0; i < rpp; ++i) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * rpp + i;
+    if (r >= rows) break;
+    RowTile<T, EPT> tile;
+    // Out-of-row lanes hold 0, which adds nothing to the sum of squares.
+    tile.load(x + r * xrs, cols, t, nt, vec, 0.f);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) ss = __builtin_fmaf(tile.v[e], tile.v[e], ss);
+    ss = block_reduce<false>(ss, part, slot, nwaves);
+    const float inv_rms = rsqrtf(ss * inv_cols + eps);
+    tile.store(y + r * yrs, cols, t, nt, vec,
+               [inv_rms, &g](float v, int e) { return (v * inv_rms) * g.v[e]; });
+  }
+}
+
+// Elements-per-lane dispatch: EPT = block_size / (waves*64) must be one of
+// the instantiated powers of two.
+template <typename T, typename Launch>
+int dispatch_ept(int ept, Launch&& launch) {
+  switch (ept) {
+    case 1: return launch(std::integral_constant<int, 1>{});
+    case 2: return launch(std::integral_constant<int, 2>{});
+    case 4: return launch(std::integral_constant<int, 4>{});
+    case 8: return launch(std::integral_constant<int, 8>{});
+    case 16: return launch(std::integral_constant<int, 16>{});
+    case 32: return launch(std::integral_constant<int, 32>{});
+    case 64: return launch(std::integral_constant<int, 64>{});
+    default:
+      set_error("no row-kernel instantiation holds %d elements per lane (1..64, powers of two)",
+                ept);
+      return KF_ERR_NOT_BUILT;
+  }
+}
+
+int check_row_config(int64_t rows, int64_t cols, int64_t xrs, int64_t yrs, int block_size,
+                     int rpp, int waves, int* ept) {
+  if (rows < 0 || cols < 0) {
+    set_error("negative shape rows=%lld cols=%lld", (long long)rows, (long long)cols);
+    return KF_ERR_INVALID_ARGUMENT;
+  }
+  if (waves < 1 || waves > kMaxWaves) {
+    set_error("waves=%d outside 1..%d (workgroup limit of 1024 lanes)", waves, kMaxWaves);
+    return KF_ERR_OUT_OF_RESOURCES;
+  }
+  if (rpp < 1) {
+    set_error("rows_per_program=%d must be positive", rpp);
+    return KF_ERR_INVALID_ARGUMENT;
+  }
+  if (block_size < 1 || (block_size & (block_size - 1)) != 0) {
+    set_error("block_size=%d is not a power of two", block_size);
+    return KF_ERR_INVALID_ARGUMENT;
+  }
+  if (block_size < cols) {
+    set_error("block_size=%d cannot hold a row of %lld", block_size, (long long)cols);
+    return KF_ERR_INVALID_ARGUMENT;
+  }
+  // A row narrower than the workgroup leaves lanes idle (one element each,
+  // masked); the search space rejects that for tuning, the kernel accepts it.
+  if (block_size >= waves * kWave && block_size % (waves * kWave) != 0) {
+    set_error("block_size=%d is not a whole number of elements per lane at waves=%d",
+              block_size, waves);
+    return KF_ERR_OUT_OF_RESOURCES;
+  }
+  if (xrs < cols || yrs < cols) {
+    set_error("row strides (%lld, %lld) shorter than the row (%lld)", (long long)xrs,
+              (long long)yrs, (long long)cols);
+    return KF_ERR_INVALID_ARGUMENT;
+  }
+  *ept = block_size >= waves * kWave ? block_size / (waves * kWave) : 1;
+  return KF_OK;
+}
+
+template <typename T>
+int launch_softmax(const void* x, void* y, int64_t rows, int64_t cols, int64_t xrs, int64_t yrs,
+                   int ept, int rpp, int waves, hipStream_t s) {
+  const bool vec = aligned16(x) && aligned16(y) && (xrs * sizeof(T)) % 16 == 0 &&
+                   (yrs * sizeof(T)) % 16 == 0;
+  const dim3 grid(static_cast<unsigned>(ceil_div(rows, rpp)));
+  const dim3 block(waves * kWave);
+  return dispatch_ept<T>(ept, [&](auto e) -> int {
+    constexpr int E = decltype(e)::value;
+    hipLaunchKernelGGL((softmax_rows<T, E>), grid, block, 0, s, static_cast<const T*>(x),
+                       static_cast<T*>(y), xrs, yrs, rows, cols, rpp, vec ? 1 : 0);
+    return launch_status("softmax");
+  });
+}
+
+template <typename T>
+int launch_rmsnorm(const void* x, const void* g, void* y, int64_t rows, int64_t cols,
+                   int64_t xrs, int64_t yrs, float eps, int ept, int rpp, int waves,
+                   hipStream_t s) {
+  const bool vec = aligned16(x) && aligned16(y) && aligned16(g) &&
+                   (xrs * sizeof(T)) % 16 == 0 && (yrs * sizeof(T)) % 16 == 0;
+  const dim3 grid(static_cast<unsigned>(ceil_div(rows, rpp)));
+  const dim3 block(waves * kWave);
+  return dispatch_ept<T>(ept, [&](auto e) -> int {
+    constexpr int E = decltype(e)::value;
+    hipLaunchKernelGGL((rmsnorm_rows<T, E>), grid, block, 0, s, static_cast<const T*>(x),
+                       static_cast<const T*>(g), static_cast<T*>(y), xrs, yrs, rows, cols, eps,
+                       rpp, vec ? 1 : 0);
+    return launch_status("rmsnorm");
+  });
+}
+
+}  // namespace
+}  // namespace kf
+
+extern "C" int kf_softmax(int dtype, const void* x, void* y, int64_t rows, int64_t cols,
+                          int64_t x_row_stride, int64_t y_row_stride, int block_size,
+                          int rows_per_program, int waves, void* stream) {
+  using namespace kf;
+  int ept = 0;
+  int rc = check_row_config(rows, cols, x_row_stride, y_row_stride, block_size, rows_per_program,
+                            waves, &ept);
+  if (rc != KF_OK) return rc;
+  if (rows == 0 || cols == 0) return KF_OK;
+  if (!x || !y) {
+    set_error("softmax: null pointer");
+    return KF_ERR_INVALID_ARGUMENT;
+  }
+  auto s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case KF_DTYPE_F32:
+      return launch_softmax<float>(x, y, rows, cols, x_row_stride, y_row_stride, ept,
+                                   rows_per_program, waves, s);
+    case KF_DTYPE_F16:
+      return launch_softmax<f16>(x, y, rows, cols, x_row_stride, y_row_stride, ept,
+                                 rows_per_program, waves, s);
+    case KF_DTYPE_BF16:
+      return launch_softmax<bf16>(x, y, rows, cols, x_row_stride, y_row_stride, ept,
+                                  rows_per_program, waves, s);
+    default:
+      set_error("softmax: unsupported dtype code %d", dtype);
+      return KF_ERR_UNSUPPORTED_DTYPE;
+  }
+}
+
+extern "C" int kf_rmsnorm(int dtype, const void* x, const void* gamma, void* y, int64_t rows,
+                          int64_t cols, int64_t x_row_stride, int64_t y_row_stride, float eps,
+                          int block_size, int rows_per_program, int waves, void* stream) {
+  using namespace kf;
+  int ept = 0;
+  int rc = check_row_config(rows, cols, x_row_stride, y_row_stride, block_size, rows_per_program,
+                            waves, &ept);
+  if (rc != KF_OK) return rc;
+  if (!(eps >= 0.f)) {
+    set_error("rmsnorm: eps must be non-negative");
+    return KF_ERR_INVALID_ARGUMENT;
+  }
+  if (rows == 0 || cols == 0) return KF_OK;
+  if (!x || !gamma || !y) {
+    set_error("rmsnorm: null pointer");
+    return KF_ERR_INVALID_ARGUMENT;
+  }
+  auto s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case KF_DTYPE_F32:
+      return launch_rmsnorm<float>(x, gamma, y, rows, cols, x_row_stride, y_row_stride, eps, ept,
+                                   rows_per_program, waves, s);
+    case KF_DTYPE_F16:
+      return launch_rmsnorm<f16>(x, gamma, y, rows, cols, x_row_stride, y_row_stride, eps, ept,
+                                 rows_per_program, waves, s);
+    case KF_DTYPE_BF16:
+      return launch_rmsnorm<bf16>(x, gamma, y, rows, cols, x_row_stride, y_row_stride, eps, ept,
+                                  rows_per_program, waves, s);
+    default:
+      set_error("rmsnorm: unsupported dtype code %d", dtype);
+      return KF_ERR_UNSUPPORTED_DTYPE;
+  }
+}

@@ -1,0 +1,49 @@
+"""Kernel registry and the public kernel entry points.
+
+Operators resolve lazily by name (kernelforge/kernels/__init__.py:17-38), so
+``import kernelo_amd.kernels`` never loads ``libkernelo_amd.so`` or creates a
+HIP context; the library loads on the first kernel call.
+"""
+
+from __future__ import annotations
+
+import importlib
+from typing import TYPE_CHECKING, Any
+
+if TYPE_CHECKING:
+    from kernelo_amd.kernels.base import Operator
+
+_OPERATORS: dict[str, tuple[str, str]] = {
+    "softmax": ("kernelo_amd.kernels.softmax", "SoftmaxOperator"),
+    "matmul": ("kernelo_amd.kernels.matmul", "MatmulOperator"),
+    "rmsnorm": ("kernelo_amd.kernels.rmsnorm", "RMSNormOperator"),
+    "fused_linear": ("kernelo_amd.kernels.fused_linear", "FusedLinearOperator"),
+}
+
+_FUNCTIONS: dict[str, str] = {
+    "matmul": "kernelo_amd.kernels.matmul",
+    "fused_linear_gelu": "kernelo_amd.kernels.fused_linear",
+    "softmax": "kernelo_amd.kernels.softmax",
+    "rmsnorm": "kernelo_amd.kernels.rmsnorm",
+}
+
+
+def operator_names() -> tuple[str, ...]:
+    return tuple(_OPERATORS)
+
+
+def get_operator(name: str) -> Operator:
+    try:
+        module_path, class_name = _OPERATORS[name]
+    except KeyError:
+        raise ValueError(
+            f"unknown operator {name!r}; available: {', '.join(operator_names())}"
+        ) from None
+    module = importlib.import_module(module_path)
+    return getattr(module, class_name)()
+
+
+def __getattr__(name: str) -> Any:
+    if name in _FUNCTIONS:
+        return getattr(importlib.import_module(_FUNCTIONS[name]), name)
+    raise AttributeError(f"module {__name__!r} has no attribute {name!r}")

@@ -1,0 +1,527 @@
+"""Candidate generation, re-derived for gfx950.
+
+The pipeline is the reference's (kernelforge/tuning/search.py:122-217):
+enumerate a grid, reject each infeasible point with a *named* rule, drop
+launches that cannot fill half the GPU (only when some candidate can), sort by
+a documented priority and keep a budget. What changes is every number and
+every rule: they come from the MI355X / CDNA4 machine model, not from an
+NVIDIA SM.
+
+Rules come in two kinds, kept apart as in the reference:
+
+* **Instantiation rules** depend only on the tile and the dtype. They decide
+  which configurations are compiled ahead of time (the build generates the
+  HIP instantiation list from :func:`gemm_instantiations`), so a grid point
+  they reject can never reach the device. These are hardware limits (LDS per
+  workgroup, MFMA shapes, the per-lane register file) and one stated register
+  budget heuristic.
+* **Problem rules** depend on the shape (tile overshoot, split-K slices too
+  short to fill a wave, rows per program beyond the row count).
+
+Nothing here imports torch.cuda state beyond :class:`DeviceCaps`, so every rule
+is unit-testable on a CPU-only host.
+"""
+
+from __future__ import annotations
+
+from abc import ABC, abstractmethod
+from collections.abc import Iterator
+from itertools import product
+
+from kernelo_amd.dtypes import itemsize
+from kernelo_amd.runtime.env import DeviceCaps, device_caps
+from kernelo_amd.tuning.config import KernelConfig, Problem
+
+#: Default candidate budget per problem (search.py:46 in the reference).
+DEFAULT_MAX_CANDIDATES = 48
+
+#: gfx950 MFMA output fragment: v_mfma_f32_16x16x32_{f16,bf16} and
+#: v_mfma_f32_16x16x4_f32 all produce 16x16 fp32 tiles.
+MFMA_TILE = 16
+
+#: k consumed per MFMA step per fragment: 4 lane groups x 16 bytes of operand.
+MFMA_K = {2: 32, 4: 16}
+
+#: Hardware limit: bytes of one vector global load / LDS row pad.
+VECTOR_BYTES = 16
+
+#: Efficiency heuristic bounded by a hardware limit. A lane has 512 registers
+#: (256 VGPR + 256 AGPR) at one wave per SIMD. fp32 accumulators above 128 per
+#: lane leave too little room for the A/B fragments and the next slice's
+#: staged global loads without spilling; 128 is a judgement, not a device
+#: property (the compiled 256x128x64 / 4-wave tile uses 228 VGPR + 136 AGPR).
+MAX_ACC_REGS_PER_LANE = 128
+
+#: Efficiency heuristic: total per-lane registers the tile model may claim
+#: (accumulators + fragments + staged global loads), leaving 64 of the 512
+#: for addresses, loop state and the epilogue.
+MAX_TILE_REGS_PER_LANE = 448
+
+
+def next_power_of_2(n: int) -> int:
+    if n < 1:
+        raise ValueError(f"expected a positive integer, got {n}")
+    return 1 << (n - 1).bit_length()
+
+
+def ceil_div(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+class SearchSpace(ABC):
+    """The set of configurations worth trying for one operation."""
+
+    operation: str
+
+    def __init__(self, max_candidates: int = DEFAULT_MAX_CANDIDATES) -> None:
+        if max_candidates < 1:
+            raise ValueError(f"max_candidates must be positive, got {max_candidates}")
+        self.max_candidates = max_candidates
+
+    @abstractmethod
+    def grid(self, problem: Problem) -> Iterator[KernelConfig]:
+        """Every point in the unfiltered parameter grid."""
+
+    @abstractmethod
+    def reject_reason(self, config: KernelConfig, problem: Problem, caps: DeviceCaps) -> str | None:
+        """Why ``config`` is not worth trying, or ``None`` to keep it."""
+
+    def num_programs(self, config: KernelConfig, problem: Problem) -> int:
+        """Workgroups in the launch grid, used by the utilisation prune."""
+        raise NotImplementedError
+
+    def priority(
+        self, config: KernelConfig, problem: Problem, caps: DeviceCaps
+    ) -> tuple[float, ...]:
+        """Sort key for the budget; lower sorts first. Ties break on the JSON form."""
+        return (0.0,)
+
+    def candidates(
+        self,
+        problem: Problem,
+        caps: DeviceCaps | None = None,
+        *,
+        max_candidates: int | None = None,
+    ) -> list[KernelConfig]:
+        return self.generate(problem, caps, max_candidates=max_candidates).candidates
+
+    def generate(
+        self,
+        problem: Problem,
+        caps: DeviceCaps | None = None,
+        *,
+        max_candidates: int | None = None,
+    ) -> CandidateSet:
+        if problem.operation != self.operation:
+            raise ValueError(
+                f"{type(self).__name__} handles {self.operation!r}, got {problem.operation!r}"
+            )
+        caps = caps if caps is not None else device_caps()
+        budget = max_candidates if max_candidates is not None else self.max_candidates
+        if budget < 1:
+            raise ValueError(f"max_candidates must be positive, got {budget}")
+
+        rejected: list[tuple[KernelConfig, str]] = []
+        kept: list[KernelConfig] = []
+        generated = 0
+        for config in self.grid(problem):
+            generated += 1
+            reason = self.reject_reason(config, problem, caps)
+            if reason is None:
+                kept.append(config)
+            else:
+                rejected.append((config, reason))
+
+        feasible = len(kept)
+        kept, pruned = self._prune_underutilised(kept, problem, caps)
+        rejected.extend(pruned)
+        kept.sort(key=lambda c: (*self.priority(c, problem, caps), c.to_json()))
+        return CandidateSet(
+            problem=problem,
+            generated=generated,
+            feasible=feasible,
+            after_prune=len(kept),
+            budget=budget,
+            candidates=kept[:budget],
+            rejected=tuple(rejected),
+        )
+
+    def _prune_underutilised(
+        self, configs: list[KernelConfig], problem: Problem, caps: DeviceCaps
+    ) -> tuple[list[KernelConfig], list[tuple[KernelConfig, str]]]:
+        """Drop launches that fill under half the CUs, unless none fills them all."""
+        try:
+            programs = {c: self.num_programs(c, problem) for c in configs}
+        except NotImplementedError:
+            return configs, []
+        if not programs or max(programs.values()) < caps.cu_count:
+            return configs, []
+        floor = caps.cu_count // 2
+        kept = [c for c in configs if programs[c] >= floor]
+        dropped = [
+            (c, f"launch grid of {programs[c]} workgroups fills under half of {caps.cu_count} CUs")
+            for c in configs
+            if programs[c] < floor
+        ]
+        return kept, dropped
+
+    def explain(self, problem: Problem, caps: DeviceCaps | None = None) -> str:
+        """Human-readable breakdown of the filtering, for ``tune --explain``."""
+        resolved = caps if caps is not None else device_caps()
+        result = self.generate(problem, resolved)
+        suffix = "" if resolved.measured else "  <- no device attached"
+        lines = [
+            f"{problem.describe()}",
+            f"  device           : {resolved.name} ({resolved.arch}), {resolved.cu_count} CUs, "
+            f"{resolved.lds_per_workgroup // 1024} KiB LDS/workgroup, "
+            f"wave{resolved.wave_size}{suffix}",
+            f"  grid points      : {result.generated}",
+            f"  feasible         : {result.feasible}",
+            f"  after prune      : {result.after_prune}",
+            f"  selected (budget): {len(result.candidates)} of {result.budget}",
+        ]
+        reasons: dict[str, int] = {}
+        for _, reason in result.rejected:
+            key = reason.split(":")[0].split("(")[0].strip()
+            reasons[key] = reasons.get(key, 0) + 1
+        if reasons:
+            lines.append("  rejections by rule:")
+            lines.extend(
+                f"    {count:>4}  {reason}"
+                for reason, count in sorted(reasons.items(), key=lambda kv: (-kv[1], kv[0]))
+            )
+        return "\n".join(lines)
+
+
+class CandidateSet:
+    """Candidates plus the counts at each stage of generation."""
+
+    __slots__ = (
+        "problem",
+        "generated",
+        "feasible",
+        "after_prune",
+        "budget",
+        "candidates",
+        "rejected",
+    )
+
+    def __init__(
+        self,
+        *,
+        problem: Problem,
+        generated: int,
+        feasible: int,
+        after_prune: int,
+        budget: int,
+        candidates: list[KernelConfig],
+        rejected: tuple[tuple[KernelConfig, str], ...],
+    ) -> None:
+        self.problem = problem
+        self.generated = generated
+        self.feasible = feasible
+        self.after_prune = after_prune
+        self.budget = budget
+        self.candidates = candidates
+        self.rejected = rejected
+
+    def __len__(self) -> int:
+        return len(self.candidates)
+
+    def __iter__(self) -> Iterator[KernelConfig]:
+        return iter(self.candidates)
+
+
+# ---------------------------------------------------------------------------
+# GEMM (matmul, fused_linear): MFMA tiles, plus split-K GEMV for decode rows.
+# ---------------------------------------------------------------------------
+
+
+def wave_grid(waves: int, block_m: int, block_n: int) -> tuple[int, int]:
+    """How the kernel arranges its waves over the tile (gemm_impl.h WaveGrid)."""
+    if waves == 4:
+        return 2, 2
+    if waves == 8:
+        return (4, 2) if block_m >= block_n else (2, 4)
+    return 1, waves
+
+
+def gemm_lds_bytes(block_m: int, block_n: int, block_k: int, stages: int, elem: int) -> int:
+    """LDS of the double-buffered A/B stages, k-contiguous rows padded by 16 bytes."""
+    pad = VECTOR_BYTES // elem
+    return stages * (block_m + block_n) * (block_k + pad) * elem
+
+
+def gemm_tile_regs(block_m: int, block_n: int, block_k: int, waves: int, elem: int) -> dict[str, int]:
+    """Per-lane register model of one tile: accumulators, fragments, staged loads."""
+    lanes = waves * 64
+    wm, wn = wave_grid(waves, block_m, block_n)
+    acc = block_m * block_n // lanes
+    frags = 4 * (block_m // wm // MFMA_TILE + block_n // wn // MFMA_TILE)
+    staged = 4 * ceil_div((block_m + block_n) * block_k * elem, VECTOR_BYTES * lanes)
+    return {"acc": acc, "frags": frags, "staged": staged, "total": acc + frags + staged}
+
+
+def gemm_instantiation_reason(
+    block_m: int, block_n: int, block_k: int, waves: int, stages: int, elem: int, caps: DeviceCaps
+) -> str | None:
+    """Shape-independent rules: why this tile is not compiled, or ``None``."""
+    kstep = MFMA_K[elem]
+    if block_k % kstep:
+        return f"MFMA k step: BLOCK_K={block_k} is not a multiple of {kstep} for {elem}-byte inputs"
+    wm, wn = wave_grid(waves, block_m, block_n)
+    if block_m % (MFMA_TILE * wm) or block_n % (MFMA_TILE * wn):
+        return (
+            f"wave tile: {block_m}x{block_n} over {wm}x{wn} waves is not whole "
+            f"{MFMA_TILE}x{MFMA_TILE} MFMA fragments"
+        )
+    lds = gemm_lds_bytes(block_m, block_n, block_k, stages, elem)
+    if lds > caps.lds_per_workgroup:
+        return (
+            f"LDS: {lds // 1024} KiB of A/B stages exceeds the "
+            f"{caps.lds_per_workgroup // 1024} KiB per-workgroup limit"
+        )
+    regs = gemm_tile_regs(block_m, block_n, block_k, waves, elem)
+    if regs["acc"] > MAX_ACC_REGS_PER_LANE:
+        return f"register pressure: {regs['acc']} accumulator registers per lane"
+    if regs["total"] > MAX_TILE_REGS_PER_LANE:
+        return f"register file: {regs['total']} tile registers per lane"
+    return None
+
+
+class _GemmSpace(SearchSpace):
+    """Shared by matmul and fused_linear: same main loop, different epilogue."""
+
+    BLOCK_M = (32, 64, 128, 256)
+    BLOCK_N = (32, 64, 128, 256)
+    BLOCK_K = (16, 32, 64)
+    NUM_WARPS = (4, 8)
+    NUM_STAGES = (2,)
+    GROUP_M = 8
+
+    #: Split-K GEMV grid, offered when M is at most GEMV_MAX_M.
+    GEMV_MAX_M = 8
+    SPLIT_K = (1, 2, 4, 8, 16, 32, 64)
+    GEMV_WARPS = (1, 2, 4, 8, 16)
+    #: Rows of W each wave keeps in flight per trip (gemv.hip kGemvUnroll).
+    GEMV_UNROLL = 8
+    #: Dynamic LDS the GEMV wave reduction may use (gemv.hip kGemvMaxLds).
+    GEMV_MAX_LDS = 64 * 1024
+
+    def grid(self, problem: Problem) -> Iterator[KernelConfig]:
+        for bm, bn, bk, warps, stages in product(
+            self.BLOCK_M, self.BLOCK_N, self.BLOCK_K, self.NUM_WARPS, self.NUM_STAGES
+        ):
+            yield KernelConfig(
+                self.operation,
+                BLOCK_M=bm,
+                BLOCK_N=bn,
+                BLOCK_K=bk,
+                GROUP_M=self.GROUP_M,
+                num_warps=warps,
+                num_stages=stages,
+            )
+        if problem.dims_dict["M"] <= self.GEMV_MAX_M:
+            for split, warps in product(self.SPLIT_K, self.GEMV_WARPS):
+                yield KernelConfig(self.operation, GEMV=1, SPLIT_K=split, num_warps=warps)
+
+    def num_programs(self, config: KernelConfig, problem: Problem) -> int:
+        dims = problem.dims_dict
+        if config.get("GEMV"):
+            strip = 64 * (VECTOR_BYTES // problem.itemsize)
+            return ceil_div(dims["N"], strip) * config["SPLIT_K"]
+        return ceil_div(dims["M"], config["BLOCK_M"]) * ceil_div(dims["N"], config["BLOCK_N"])
+
+    def reject_reason(self, config: KernelConfig, problem: Problem, caps: DeviceCaps) -> str | None:
+        dims = problem.dims_dict
+        m, n, k = dims["M"], dims["N"], dims["K"]
+        elem = itemsize(problem.dtype)
+        if config.get("GEMV"):
+            return self._gemv_reason(config, m, k, elem)
+
+        bm, bn = config["BLOCK_M"], config["BLOCK_N"]
+        reason = gemm_instantiation_reason(
+            bm, bn, config["BLOCK_K"], config["num_warps"], config["num_stages"], elem, caps
+        )
+        if reason is not None:
+            return reason
+        # A tile more than twice the problem computes thrown-away work. As in
+        # the reference (search.py:370-386), the rule yields while no smaller
+        # tile exists in the grid, so tiny problems keep a candidate.
+        if bm > 2 * m and bm > min(self.BLOCK_M):
+            return f"tile overshoot: BLOCK_M={bm} for M={m}"
+        if bn > 2 * n and bn > min(self.BLOCK_N):
+            return f"tile overshoot: BLOCK_N={bn} for N={n}"
+        return None
+
+    def _gemv_reason(self, config: KernelConfig, m: int, k: int, elem: int) -> str | None:
+        warps, split = config["num_warps"], config["SPLIT_K"]
+        mr = next_power_of_2(m)
+        lds = warps * mr * 64 * (VECTOR_BYTES // elem) * 4
+        if lds > self.GEMV_MAX_LDS:
+            return f"LDS: wave reduction needs {lds // 1024} KiB at num_warps={warps}, M={m}"
+        slice_rows = ceil_div(k, split)
+        if split > 1 and slice_rows < warps * self.GEMV_UNROLL:
+            return (
+                f"split-K slice too short: {slice_rows} rows of K for {warps} waves x "
+                f"{self.GEMV_UNROLL} rows in flight"
+            )
+        return None
+
+    def priority(
+        self, config: KernelConfig, problem: Problem, caps: DeviceCaps
+    ) -> tuple[float, ...]:
+        """Rank survivors for the budget.
+
+        GEMM tiles: (1) workgroups, saturating at one per CU, so that a large
+        problem ties and a small one prefers filling the GPU; (2) reuse
+        ``BM*BN/(BM+BN)`` -- the MFMA work per byte staged through LDS;
+        (3) least padding waste; then fewer waves (more registers each).
+        GEMV: HBM-bound, so (1) at least one workgroup per CU, (2) at least
+        eight waves per CU (each keeps 8 x 1 KiB row segments in flight, and
+        HBM needs ~32 KiB in flight per CU), then fewer slices (less partial-sum
+        traffic) and fewer waves. GEMV candidates sort ahead of MFMA tiles for
+        decode shapes.
+        """
+        dims = problem.dims_dict
+        programs = self.num_programs(config, problem)
+        if config.get("GEMV"):
+            waves = programs * config["num_warps"]
+            return (
+                0,
+                -min(programs, caps.cu_count),
+                -min(waves, 8 * caps.cu_count),
+                config["SPLIT_K"],
+                config["num_warps"],
+            )
+        bm, bn = config["BLOCK_M"], config["BLOCK_N"]
+        reuse = (bm * bn) / (bm + bn)
+        padded = ceil_div(dims["M"], bm) * bm * ceil_div(dims["N"], bn) * bn
+        waste = padded / (dims["M"] * dims["N"])
+        return (1, -min(programs, caps.cu_count), -reuse, waste, config["num_warps"])
+
+
+class MatmulSearchSpace(_GemmSpace):
+    operation = "matmul"
+
+
+class FusedLinearSearchSpace(_GemmSpace):
+    operation = "fused_linear"
+
+
+def gemm_instantiations(caps: DeviceCaps | None = None) -> dict[int, list[tuple[int, ...]]]:
+    """Tile configs the build compiles, keyed by element size in bytes.
+
+    Every (BLOCK_M, BLOCK_N, BLOCK_K, num_warps, num_stages) point of the
+    GEMM grid that passes the shape-independent rules.
+    """
+    from kernelo_amd.runtime.env import MI355X_CAPS
+
+    caps = caps if caps is not None else MI355X_CAPS
+    space = _GemmSpace
+    out: dict[int, list[tuple[int, ...]]] = {}
+    for elem in (2, 4):
+        out[elem] = [
+            (bm, bn, bk, w, s)
+            for bm, bn, bk, w, s in product(
+                space.BLOCK_M, space.BLOCK_N, space.BLOCK_K, space.NUM_WARPS, space.NUM_STAGES
+            )
+            if gemm_instantiation_reason(bm, bn, bk, w, s, elem, caps) is None
+        ]
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Row kernels (softmax, rmsnorm): one pass, whole row in registers.
+# ---------------------------------------------------------------------------
+
+
+class _RowReductionSpace(SearchSpace):
+    """Shared by softmax and rmsnorm.
+
+    BLOCK_SIZE is fixed by the row width (the row must fit), which leaves the
+    wave count and the rows per workgroup free (search.py:422-503).
+    """
+
+    NUM_WARPS = (1, 2, 4, 8, 16)
+    ROWS_PER_PROGRAM = (1, 2, 4, 8)
+
+    #: fp32 values a lane holds for its share of the row. Hardware-derived:
+    #: 64 of the 256 VGPRs, leaving the rest for gamma (RMSNorm) and addresses.
+    MIN_ELEMS_PER_LANE = 1
+    MAX_ELEMS_PER_LANE = 64
+
+    #: Widest single-pass row: 64 values x 1024 lanes (16 waves, the
+    #: workgroup limit). The default configuration reaches exactly
+    #: MAX_ELEMS_PER_LANE at this width, mirroring the reference's tie
+    #: between its limit and its default (search.py:441-459).
+    MAX_WAVES = 16
+    MAX_BLOCK_SIZE = MAX_ELEMS_PER_LANE * MAX_WAVES * 64
+
+    def grid(self, problem: Problem) -> Iterator[KernelConfig]:
+        block = next_power_of_2(problem.dims_dict["cols"])
+        for warps, rows in product(self.NUM_WARPS, self.ROWS_PER_PROGRAM):
+            yield KernelConfig(
+                self.operation, BLOCK_SIZE=block, ROWS_PER_PROGRAM=rows, num_warps=warps
+            )
+
+    def num_programs(self, config: KernelConfig, problem: Problem) -> int:
+        return ceil_div(problem.dims_dict["rows"], config["ROWS_PER_PROGRAM"])
+
+    def reject_reason(self, config: KernelConfig, problem: Problem, caps: DeviceCaps) -> str | None:
+        block = config["BLOCK_SIZE"]
+        if block > self.MAX_BLOCK_SIZE:
+            return f"row of {problem.dims_dict['cols']} exceeds the single-pass limit"
+        lanes = config["num_warps"] * caps.wave_size
+        if lanes > caps.max_threads_per_workgroup:
+            return f"workgroup size: {lanes} lanes exceeds {caps.max_threads_per_workgroup}"
+        per_lane = block / lanes
+        if per_lane < self.MIN_ELEMS_PER_LANE:
+            return f"idle lanes: {lanes} lanes for BLOCK_SIZE={block}"
+        if per_lane > self.MAX_ELEMS_PER_LANE:
+            return f"register pressure: {per_lane:.0f} elements per lane"
+        rows = problem.dims_dict["rows"]
+        if config["ROWS_PER_PROGRAM"] > rows:
+            return f"ROWS_PER_PROGRAM={config['ROWS_PER_PROGRAM']} exceeds {rows} rows"
+        return None
+
+    def priority(
+        self, config: KernelConfig, problem: Problem, caps: DeviceCaps
+    ) -> tuple[float, ...]:
+        """Fill the CUs first, then 8-16 elements per lane (two 16-byte loads in
+        flight per lane), then fewer rows per program."""
+        programs = min(self.num_programs(config, problem), caps.cu_count)
+        per_lane = config["BLOCK_SIZE"] / (config["num_warps"] * caps.wave_size)
+        return (-programs, abs(per_lane - 12), config["ROWS_PER_PROGRAM"])
+
+
+class SoftmaxSearchSpace(_RowReductionSpace):
+    operation = "softmax"
+
+
+class RMSNormSearchSpace(_RowReductionSpace):
+    operation = "rmsnorm"
+
+
+def default_row_config(operation: str, n_cols: int) -> KernelConfig:
+    """One wave per 512 columns, up to 16 waves; one row per workgroup."""
+    block = next_power_of_2(n_cols)
+    warps = max(1, min(_RowReductionSpace.MAX_WAVES, block // 512))
+    return KernelConfig(operation, BLOCK_SIZE=block, ROWS_PER_PROGRAM=1, num_warps=warps)
+
+
+SEARCH_SPACES: dict[str, type[SearchSpace]] = {
+    "softmax": SoftmaxSearchSpace,
+    "matmul": MatmulSearchSpace,
+    "rmsnorm": RMSNormSearchSpace,
+    "fused_linear": FusedLinearSearchSpace,
+}
+
+
+def search_space(operation: str, **kwargs) -> SearchSpace:
+    try:
+        return SEARCH_SPACES[operation](**kwargs)
+    except KeyError:
+        raise ValueError(
+            f"no search space for {operation!r}; known: {sorted(SEARCH_SPACES)}"
+        ) from None

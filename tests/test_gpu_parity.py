@@ -1,0 +1,347 @@
+"""GPU parity: every HIP kernel against the CPU oracle on the same seeded inputs.
+
+Inputs are drawn on the CPU (torch.Generator().manual_seed), copied to the
+device, run through the C-ABI via the kernel wrappers, copied back and gated
+with the reference's normalised infinity norm at the reference's per-dtype
+thresholds (fp32 1e-5, fp16 5e-3, bf16 2e-2; kernelforge/testing.py:31-35).
+Shapes are the reference's correctness suites (workloads.py:65-105) plus the
+BASELINE configurations at sizes the oracle finishes in seconds.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from kernelo_amd.benchmark.workloads import MATMUL_SHAPES, ROW_SHAPES
+from kernelo_amd.testing import verify
+from kernelo_amd.tuning.config import KernelConfig
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+DEV = "cuda"
+
+
+def _randn(*shape, dtype, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g, dtype=torch.float32) * scale).to(dtype)
+
+
+def _gate(ref: torch.Tensor, out: torch.Tensor, dtype: torch.dtype, what: str) -> None:
+    res = verify(ref, out.cpu(), dtype=dtype)
+    assert res.passed, f"{what}: {res.reason}"
+
+
+# --- RMSNorm -------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("rows,cols", ROW_SHAPES["correctness"])
+def test_rmsnorm_correctness_suite(rows, cols, dtype):
+    from kernelo_amd.kernels.rmsnorm import rmsnorm
+
+    x = _randn(rows, cols, dtype=dtype, seed=rows * 7 + cols)
+    g = (_randn(cols, dtype=torch.float32, seed=cols) * 0.1 + 1.0).to(dtype)
+    out = rmsnorm(x.to(DEV), g.to(DEV), eps=1e-5)
+    _gate(ops.rmsnorm_ref(x, g, 1e-5), out, dtype, f"rmsnorm {rows}x{cols}")
+
+
+@pytest.mark.parametrize("warps", (1, 2, 4, 8, 16))
+@pytest.mark.parametrize("rpp", (1, 2, 4, 8))
+def test_rmsnorm_configs(warps, rpp):
+    """Every wave count and rows-per-program, including tails of the row loop."""
+    from kernelo_amd.kernels.rmsnorm import rmsnorm
+
+    rows, cols = 333, 4096
+    x = _randn(rows, cols, dtype=torch.float16, seed=3)
+    g = (_randn(cols, dtype=torch.float32, seed=4) * 0.1 + 1.0).to(torch.float16)
+    cfg = KernelConfig("rmsnorm", BLOCK_SIZE=4096, ROWS_PER_PROGRAM=rpp, num_warps=warps)
+    out = rmsnorm(x.to(DEV), g.to(DEV), config=cfg)
+    _gate(ops.rmsnorm_ref(x, g), out, torch.float16, str(cfg))
+
+
+def test_rmsnorm_baseline_config_fp32():
+    """x[4096,4096] ~ N(0,1), gamma ~ N(1, 0.1), eps=1e-6, fp32."""
+    from kernelo_amd.kernels.rmsnorm import rmsnorm
+
+    g0 = torch.Generator().manual_seed(0)
+    x = torch.randn(4096, 4096, generator=g0)
+    gamma = 1.0 + 0.1 * torch.randn(4096, generator=g0)
+    out = rmsnorm(x.to(DEV), gamma.to(DEV), eps=1e-6)
+    _gate(ops.rmsnorm_ref(x, gamma, 1e-6), out, torch.float32, "rmsnorm config 1")
+
+
+def test_rmsnorm_zero_row_is_zero_and_finite():
+    from kernelo_amd.kernels.rmsnorm import rmsnorm
+
+    x = torch.zeros(4, 1024, dtype=torch.float16, device=DEV)
+    g = torch.ones(1024, dtype=torch.float16, device=DEV)
+    out = rmsnorm(x, g)
+    assert torch.isfinite(out).all() and (out == 0).all()
+
+
+# --- Softmax -------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("rows,cols", ROW_SHAPES["correctness"])
+def test_softmax_correctness_suite(rows, cols, dtype):
+    from kernelo_amd.kernels.softmax import softmax
+
+    x = _randn(rows, cols, dtype=dtype, seed=rows * 13 + cols, scale=3.0)
+    out = softmax(x.to(DEV))
+    _gate(ops.softmax_ref(x), out, dtype, f"softmax {rows}x{cols}")
+
+
+@pytest.mark.parametrize("cols", (4096, 11008))
+def test_softmax_overflow_rows(cols):
+    """BASELINE config 2 recipe at 512 rows: N(0,3), 1% of rows shifted by +60, fp16."""
+    from kernelo_amd.kernels.softmax import softmax
+
+    rows = 512
+    g = torch.Generator().manual_seed(0)
+    x = 3.0 * torch.randn(rows, cols, generator=g)
+    hot = torch.randperm(rows, generator=g)[: max(1, rows // 100)]
+    x[hot] += 60.0
+    x = x.to(torch.float16)
+    out = softmax(x.to(DEV))
+    assert torch.isfinite(out).all()
+    _gate(ops.softmax_ref(x), out, torch.float16, f"softmax overflow {cols}")
+    sums = out.float().sum(-1).cpu()
+    assert torch.allclose(sums, torch.ones_like(sums), atol=5e-3)
+
+
+def test_softmax_constant_row_is_exactly_one_over_n():
+    from kernelo_amd.kernels.softmax import softmax
+
+    x = torch.full((3, 4096), 7.25, dtype=torch.float16, device=DEV)
+    out = softmax(x)
+    assert (out == torch.tensor(1.0 / 4096, dtype=torch.float16)).all()
+
+
+@pytest.mark.parametrize("warps", (1, 4, 16))
+@pytest.mark.parametrize("rpp", (1, 3, 8))
+def test_softmax_configs(warps, rpp):
+    from kernelo_amd.kernels.softmax import softmax
+
+    rows, cols = 77, 2000
+    x = _randn(rows, cols, dtype=torch.bfloat16, seed=5, scale=3.0)
+    cfg = KernelConfig("softmax", BLOCK_SIZE=2048, ROWS_PER_PROGRAM=rpp, num_warps=warps)
+    out = softmax(x.to(DEV), config=cfg)
+    _gate(ops.softmax_ref(x), out, torch.bfloat16, str(cfg))
+
+
+# --- GEMM / fused linear -------------------------------------------------------
+
+_GEMM_SHAPES = [s for s in MATMUL_SHAPES["correctness"] if s[0] * s[1] * s[2] <= 2**31]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("m,n,k", _GEMM_SHAPES)
+def test_matmul_correctness_suite(m, n, k, dtype):
+    from kernelo_amd.kernels.matmul import matmul
+
+    a = _randn(m, k, dtype=dtype, seed=m + 3 * n + 7 * k)
+    b = _randn(k, n, dtype=dtype, seed=m * n + k)
+    out = matmul(a.to(DEV), b.to(DEV))
+    _gate(ops.matmul_ref(a, b), out, dtype, f"matmul {m}x{n}x{k}")
+
+
+_TILES = [
+    (32, 32, 32, 4),
+    (64, 64, 64, 4),
+    (128, 128, 64, 4),
+    (256, 128, 64, 4),
+    (128, 256, 32, 8),
+    (256, 256, 64, 8),
+    (64, 256, 64, 8),
+]
+
+
+@pytest.mark.parametrize("tile", _TILES, ids=lambda t: "x".join(map(str, t)))
+@pytest.mark.parametrize("layout", ("nn", "nt", "tn"))
+@pytest.mark.parametrize("m,n,k", [(257, 513, 129), (1023, 4097, 127), (512, 512, 512)])
+def test_matmul_tiles_and_layouts(tile, layout, m, n, k):
+    """Every loader pair: row-major B (VecN), transposed B (VecK), strided A (scalar)."""
+    from kernelo_amd.kernels.matmul import matmul
+
+    bm, bn, bk, w = tile
+    dtype = torch.float16
+    a = _randn(m, k, dtype=dtype, seed=1)
+    b = _randn(k, n, dtype=dtype, seed=2)
+    da, db = a.to(DEV), b.to(DEV)
+    if layout[1] == "t":
+        db = b.t().contiguous().to(DEV).t()
+    if layout[0] == "t":
+        da = a.t().contiguous().to(DEV).t()
+    cfg = KernelConfig(
+        "matmul", BLOCK_M=bm, BLOCK_N=bn, BLOCK_K=bk, GROUP_M=8, num_warps=w, num_stages=2
+    )
+    out = matmul(da, db, config=cfg)
+    _gate(ops.matmul_ref(a, b), out, dtype, f"{cfg} {layout} {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16), ids=("fp16", "bf16"))
+def test_matmul_baseline_config(dtype):
+    """BASELINE config 3 (fp16) and its bf16 twin: A[2048,4096] @ B[4096,4096], N(0,1)/sqrt(K)."""
+    from kernelo_amd.kernels.matmul import matmul
+
+    a = _randn(2048, 4096, dtype=dtype, seed=0, scale=4096**-0.5)
+    b = _randn(4096, 4096, dtype=dtype, seed=1, scale=4096**-0.5)
+    out = matmul(a.to(DEV), b.to(DEV))
+    _gate(ops.matmul_ref(a, b), out, dtype, "matmul config 3")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("m,n,k", [(1, 7, 3), (127, 127, 127), (257, 129, 65), (511, 769, 1025)])
+def test_fused_linear_correctness(m, n, k, dtype):
+    from kernelo_amd.kernels.fused_linear import fused_linear_gelu
+
+    x = _randn(m, k, dtype=dtype, seed=m + k)
+    w = _randn(k, n, dtype=dtype, seed=n, scale=k**-0.5)
+    bias = _randn(n, dtype=dtype, seed=7)
+    out = fused_linear_gelu(x.to(DEV), w.to(DEV), bias.to(DEV))
+    _gate(ops.linear_gelu_ref(x, w, bias), out, dtype, f"fused {m}x{n}x{k}")
+
+
+def test_fused_linear_transposed_weight():
+    """nn.Linear stores weight as (N, K); the kernel reads weight.t() through strides."""
+    from kernelo_amd.kernels.fused_linear import fused_linear_gelu
+
+    m, n, k = 300, 520, 256
+    x = _randn(m, k, dtype=torch.float16, seed=1)
+    weight = _randn(n, k, dtype=torch.float16, seed=2, scale=k**-0.5)
+    bias = _randn(n, dtype=torch.float16, seed=3)
+    out = fused_linear_gelu(x.to(DEV), weight.to(DEV).t(), bias.to(DEV))
+    _gate(ops.linear_gelu_ref(x, weight.t(), bias), out, torch.float16, "fused weight.t()")
+
+
+def test_fused_linear_identity_weight_traces_gelu():
+    """Identity weight, zero bias: the output is gelu_tanh(x) over [-60, 60] and +-1e4."""
+    from kernelo_amd.kernels.fused_linear import fused_linear_gelu
+
+    n = 128
+    vals = torch.cat([torch.linspace(-60, 60, 126), torch.tensor([-1e4, 1e4])])
+    x = torch.diag(vals).to(torch.float32)
+    w = torch.eye(n, dtype=torch.float32)
+    bias = torch.zeros(n, dtype=torch.float32)
+    out = fused_linear_gelu(x.to(DEV), w.to(DEV), bias.to(DEV)).cpu().double()
+    expect = torch.from_numpy(ops.linear_gelu_fp64(x, w, bias))
+    err = (out - expect).abs().max() / expect.abs().max()
+    assert err < 1e-4, err
+
+
+def test_fused_linear_zero_weight_is_gelu_of_bias():
+    from kernelo_amd.kernels.fused_linear import fused_linear_gelu
+
+    m, n, k = 64, 256, 64
+    x = _randn(m, k, dtype=torch.float16, seed=1)
+    w = torch.zeros(k, n, dtype=torch.float16)
+    bias = _randn(n, dtype=torch.float16, seed=2, scale=3.0)
+    out = fused_linear_gelu(x.to(DEV), w.to(DEV), bias.to(DEV)).cpu()
+    expect = torch.nn.functional.gelu(bias.float(), approximate="tanh").to(torch.float16)
+    _gate(expect.expand(m, n), out, torch.float16, "zero weight")
+
+
+# --- Decode GEMV -----------------------------------------------------------------
+
+
+@pytest.mark.parametrize("split", (1, 2, 8, 16, 64))
+@pytest.mark.parametrize("warps", (1, 4, 8, 16))
+def test_gemv_decode_config(split, warps):
+    """BASELINE config 5a: bf16 1x11008x4096, U(-1, 1)."""
+    from kernelo_amd.kernels.matmul import matmul
+
+    g = torch.Generator().manual_seed(0)
+    x = (torch.rand(1, 4096, generator=g) * 2 - 1).to(torch.bfloat16)
+    w = (torch.rand(4096, 11008, generator=g) * 2 - 1).to(torch.bfloat16)
+    cfg = KernelConfig("matmul", GEMV=1, SPLIT_K=split, num_warps=warps)
+    out = matmul(x.to(DEV), w.to(DEV), config=cfg)
+    _gate(ops.matmul_ref(x, w), out, torch.bfloat16, str(cfg))
+
+
+def test_gemv_is_deterministic():
+    from kernelo_amd.kernels.matmul import matmul
+
+    x = _randn(1, 4096, dtype=torch.bfloat16, seed=1).to(DEV)
+    w = _randn(4096, 11008, dtype=torch.bfloat16, seed=2).to(DEV)
+    cfg = KernelConfig("matmul", GEMV=1, SPLIT_K=32, num_warps=8)
+    first = matmul(x, w, config=cfg)
+    for _ in range(5):
+        assert torch.equal(matmul(x, w, config=cfg), first)
+
+
+@pytest.mark.parametrize("m", (1, 2, 3, 5, 8))
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_gemv_small_batches(m, dtype):
+    from kernelo_amd.kernels.matmul import matmul
+
+    x = _randn(m, 1000, dtype=dtype, seed=m)
+    w = _randn(1000, 3000, dtype=dtype, seed=9, scale=1000**-0.5)
+    cfg = KernelConfig("matmul", GEMV=1, SPLIT_K=4, num_warps=4)
+    out = matmul(x.to(DEV), w.to(DEV), config=cfg)
+    _gate(ops.matmul_ref(x, w), out, dtype, f"gemv m={m}")
+
+
+# --- guard bands: bit-exact masks -------------------------------------------------
+
+
+def _guarded_call(m, n, k, cfg, seed, dtype=torch.bfloat16):
+    """Run through the C-ABI with C inside a NaN-filled guard band (row pitch n+9,
+    8 guard rows above and below); return (inside, guard_intact)."""
+    import ctypes
+
+    from kernelo_amd.dtypes import abi_code
+    from kernelo_amd.runtime import hip
+
+    g = torch.Generator().manual_seed(seed)
+    a = (torch.rand(m, k, generator=g) * 2 - 1).to(dtype)
+    b = (torch.rand(k, n, generator=g) * 2 - 1).to(dtype)
+    pitch, pad = n + 9, 8
+    buf = torch.full(((m + 2 * pad) * pitch,), float("nan"), dtype=dtype, device=DEV)
+    c_off = pad * pitch
+    da, db = a.to(DEV), b.to(DEV)
+    lib = hip.load()
+    stream = hip.stream_of(da)
+    cptr = buf.data_ptr() + c_off * buf.element_size()
+    if cfg.get("GEMV"):
+        need = lib.kf_gemv_workspace_bytes(m, n, cfg["SPLIT_K"])
+        ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=DEV)
+        rc = lib.kf_gemv(abi_code(dtype), da.data_ptr(), db.data_ptr(), None, cptr, m, n, k,
+                         da.stride(0), da.stride(1), db.stride(0), db.stride(1), pitch, 1, 0,
+                         cfg["SPLIT_K"], cfg["num_warps"], ws.data_ptr(), ws.numel(), stream)
+    else:
+        rc = lib.kf_gemm(abi_code(dtype), da.data_ptr(), db.data_ptr(), None, cptr, m, n, k,
+                         da.stride(0), da.stride(1), db.stride(0), db.stride(1), pitch, 1, 0,
+                         cfg["BLOCK_M"], cfg["BLOCK_N"], cfg["BLOCK_K"], cfg["num_warps"], 2, 8,
+                         stream)
+    hip.check(rc, "guarded call")
+    torch.cuda.synchronize()
+    host = buf.cpu().view(m + 2 * pad, pitch).float()
+    inside = host[pad : pad + m, :n]
+    guard = torch.ones_like(host, dtype=torch.bool)
+    guard[pad : pad + m, :n] = False
+    return a, b, inside, bool(torch.isnan(host[guard]).all())
+
+
+@pytest.mark.parametrize(
+    "m,n,k,cfg",
+    [
+        (1023, 4097, 127, KernelConfig("matmul", BLOCK_M=128, BLOCK_N=128, BLOCK_K=32, GROUP_M=8, num_warps=4, num_stages=2)),
+        (1023, 4097, 127, KernelConfig("matmul", BLOCK_M=256, BLOCK_N=128, BLOCK_K=64, GROUP_M=8, num_warps=4, num_stages=2)),
+        (1023, 4097, 127, KernelConfig("matmul", BLOCK_M=32, BLOCK_N=64, BLOCK_K=32, GROUP_M=8, num_warps=4, num_stages=2)),
+        (1, 7, 3, KernelConfig("matmul", GEMV=1, SPLIT_K=1, num_warps=1)),
+        (1, 7, 3, KernelConfig("matmul", GEMV=1, SPLIT_K=2, num_warps=4)),
+        (1, 7, 3, KernelConfig("matmul", BLOCK_M=32, BLOCK_N=32, BLOCK_K=32, GROUP_M=8, num_warps=4, num_stages=2)),
+    ],
+    ids=lambda v: str(v) if not isinstance(v, KernelConfig) else "-".join(f"{x}" for x in v.values()),
+)
+def test_edge_shapes_guard_band(m, n, k, cfg):
+    """BASELINE config 5b/5c: every in-range element finite and within the gate,
+    every guard element still NaN (bit-for-bit masks)."""
+    a, b, inside, guard_ok = _guarded_call(m, n, k, cfg, seed=m + n + k)
+    assert guard_ok, "kernel wrote outside C"
+    assert torch.isfinite(inside).all()
+    _gate(ops.matmul_ref(a, b).float(), inside, torch.bfloat16, f"{cfg} {m}x{n}x{k}")
