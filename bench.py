@@ -88,6 +88,10 @@ def main(argv: list[str] | None = None) -> int:
     from kernelo_amd.runtime.env import device_caps, host_cores
     from kernelo_amd.testing import assert_verified, exact_fp32_matmul
 
+    from kernelo_amd.kernels import get_operator
+    from kernelo_amd.runtime.dispatch import select_config
+    from kernelo_amd.tuning.config import Problem
+
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
@@ -98,6 +102,12 @@ def main(argv: list[str] | None = None) -> int:
     steps, warmup = args.steps, args.warmup
     g = torch.Generator().manual_seed(0)
     results: dict[str, dict] = {}
+
+    def pick(operation, dtype, **dims):
+        """The config dispatch would run: user cache, packaged winners, default."""
+        sel = select_config(get_operator(operation), Problem.create(operation, dtype, **dims),
+                            device=dev)
+        return sel.config, {"config_source": sel.source, "kernel_config": dict(sel.config)}
 
     def record(name, fn, work, unit, peak, extra=None):
         samples = _time_steps(fn, steps, warmup, flush)
@@ -140,33 +150,36 @@ def main(argv: list[str] | None = None) -> int:
     x = torch.randn(4096, 4096, generator=g)
     gamma = 1.0 + 0.1 * torch.randn(4096, generator=g)
     dx, dgamma = x.to(dev), gamma.to(dev)
-    assert_verified(rmsnorm_reference(dx, dgamma, eps=1e-6), rmsnorm(dx, dgamma, eps=1e-6),
-                    context="rmsnorm config 1")
-    record("rmsnorm_fp32_4096x4096", lambda: rmsnorm(dx, dgamma, eps=1e-6),
-           metrics.rmsnorm_bytes(4096, 4096, 4), "GB/s", hbm)
+    cfg, src = pick("rmsnorm", "fp32", rows=4096, cols=4096)
+    assert_verified(rmsnorm_reference(dx, dgamma, eps=1e-6),
+                    rmsnorm(dx, dgamma, eps=1e-6, config=cfg), context="rmsnorm config 1")
+    record("rmsnorm_fp32_4096x4096", lambda: rmsnorm(dx, dgamma, eps=1e-6, config=cfg),
+           metrics.rmsnorm_bytes(4096, 4096, 4), "GB/s", hbm, src)
 
     # --- config 2: softmax fp16 [8192,4096] and [8192,11008], 1% rows +60 ---------
     for cols in (4096, 11008):
         s = 3.0 * torch.randn(8192, cols, generator=g)
         s[torch.randperm(8192, generator=g)[:82]] += 60.0
         ds = s.to(torch.float16).to(dev)
-        out = softmax(ds)
+        cfg, src = pick("softmax", "fp16", rows=8192, cols=cols)
+        out = softmax(ds, config=cfg)
         assert torch.isfinite(out).all()
         assert_verified(torch.softmax(ds.float(), -1), out, dtype=torch.float16,
                         context=f"softmax config 2 ({cols})")
-        record(f"softmax_fp16_8192x{cols}", lambda ds=ds: softmax(ds),
-               metrics.softmax_bytes(8192, cols, 2), "GB/s", hbm)
+        record(f"softmax_fp16_8192x{cols}", lambda ds=ds, cfg=cfg: softmax(ds, config=cfg),
+               metrics.softmax_bytes(8192, cols, 2), "GB/s", hbm, src)
         del ds, s
 
     # --- config 3: GEMM fp16 2048x4096x4096 (headline) -----------------------------
     M, N, K = 2048, 4096, 4096
     a = (torch.randn(M, K, generator=g) / K**0.5).to(torch.float16).to(dev)
     b = (torch.randn(K, N, generator=g) / K**0.5).to(torch.float16).to(dev)
+    gcfg, src = pick("matmul", "fp16", M=M, N=N, K=K)
     with exact_fp32_matmul():
-        assert_verified(torch.matmul(a.float(), b.float()), matmul(a, b), dtype=torch.float16,
-                        context="gemm config 3")
-    gemm = record("gemm_fp16_2048x4096x4096", lambda: matmul(a, b),
-                  metrics.matmul_flops(M, N, K), "TFLOP/s", f16_peak)
+        assert_verified(torch.matmul(a.float(), b.float()), matmul(a, b, config=gcfg),
+                        dtype=torch.float16, context="gemm config 3")
+    gemm = record("gemm_fp16_2048x4096x4096", lambda: matmul(a, b, config=gcfg),
+                  metrics.matmul_flops(M, N, K), "TFLOP/s", f16_peak, src)
     torch_gemm = _time_steps(lambda: torch.matmul(a, b), steps, warmup, flush)
     gemm["torch_hipblaslt_tflops"] = metrics.matmul_flops(M, N, K) / (np.mean(torch_gemm) * 1e-3) / 1e12
 
@@ -175,10 +188,12 @@ def main(argv: list[str] | None = None) -> int:
     fx = (torch.randn(FM, FK, generator=g) / FK**0.5).to(torch.float16).to(dev)
     fw = (torch.randn(FK, FN, generator=g) / FK**0.5).to(torch.float16).to(dev)
     fb = (0.02 * torch.randn(FN, generator=g)).to(torch.float16).to(dev)
-    assert_verified(linear_gelu_reference(fx, fw, fb), fused_linear_gelu(fx, fw, fb),
+    fcfg, src = pick("fused_linear", "fp16", M=FM, N=FN, K=FK)
+    assert_verified(linear_gelu_reference(fx, fw, fb), fused_linear_gelu(fx, fw, fb, config=fcfg),
                     context="fused linear config 4")
-    fused = record("fused_linear_fp16_4096x11008x4096", lambda: fused_linear_gelu(fx, fw, fb),
-                   metrics.matmul_flops(FM, FN, FK), "TFLOP/s", f16_peak)
+    fused = record("fused_linear_fp16_4096x11008x4096",
+                   lambda: fused_linear_gelu(fx, fw, fb, config=fcfg),
+                   metrics.matmul_flops(FM, FN, FK), "TFLOP/s", f16_peak, src)
     unfused = _time_steps(lambda: linear_gelu_reference(fx, fw, fb), steps, warmup, flush)
     fused["unfused_torch_3op_us"] = float(np.mean(unfused)) * 1e3
     fused["speedup_vs_unfused"] = float(np.mean(unfused)) * 1e3 / fused["mean_us"]
@@ -187,10 +202,11 @@ def main(argv: list[str] | None = None) -> int:
     # --- config 5a: decode GEMV bf16 1x11008x4096 ----------------------------------
     vx = (torch.rand(1, 4096, generator=g) * 2 - 1).to(torch.bfloat16).to(dev)
     vw = (torch.rand(4096, 11008, generator=g) * 2 - 1).to(torch.bfloat16).to(dev)
-    assert_verified(torch.matmul(vx.float(), vw.float()), matmul(vx, vw), dtype=torch.bfloat16,
-                    context="gemv config 5a")
-    record("gemv_bf16_1x11008x4096", lambda: matmul(vx, vw),
-           metrics.matmul_bytes(1, 11008, 4096, 2), "GB/s", hbm)
+    vcfg, src = pick("matmul", "bf16", M=1, N=11008, K=4096)
+    assert_verified(torch.matmul(vx.float(), vw.float()), matmul(vx, vw, config=vcfg),
+                    dtype=torch.bfloat16, context="gemv config 5a")
+    record("gemv_bf16_1x11008x4096", lambda: matmul(vx, vw, config=vcfg),
+           metrics.matmul_bytes(1, 11008, 4096, 2), "GB/s", hbm, src)
 
     # --- CPU baseline: the oracle on the host cores, bounded slices ----------------
     cpu = None

@@ -53,6 +53,14 @@ enum {
   KF_ERR_OUT_OF_MEMORY = -7     /* hipErrorOutOfMemory from the runtime       */
 };
 
+/* GEMM main-loop pipelines. */
+enum {
+  KF_PIPELINE_STAGED = 0, /* global -> VGPR -> LDS (padded rows), any layout      */
+  KF_PIPELINE_DIRECT = 1  /* global -> LDS DMA (swizzled rows), 16-bit aligned
+                             operands with K (and N for row-major B) % 8 == 0;
+                             other layouts fall back to the staged twin tile   */
+};
+
 /* GEMM epilogues. */
 enum {
   KF_EPILOGUE_NONE = 0,      /* C = A @ B                                     */
@@ -82,6 +90,7 @@ const char* kf_last_error(void);
  *   waves                     : wavefronts (64 lanes) per workgroup
  *   stages                    : LDS buffers (2 = double buffered)
  *   group_m                   : rows of tiles per launch-order group
+ *   pipeline                  : KF_PIPELINE_STAGED or KF_PIPELINE_DIRECT
  * Returns KF_ERR_NOT_BUILT for a tile config that was not instantiated.
  */
 int kf_gemm(int dtype, const void* A, const void* B, const void* bias, void* C,
@@ -89,16 +98,17 @@ int kf_gemm(int dtype, const void* A, const void* B, const void* bias, void* C,
             int64_t lda_m, int64_t lda_k, int64_t ldb_k, int64_t ldb_n,
             int64_t ldc_m, int64_t ldc_n, int epilogue,
             int block_m, int block_n, int block_k, int waves, int stages, int group_m,
-            void* stream);
+            int pipeline, void* stream);
 
-/* 1 if (dtype, tile config) has an instantiation in this build, else 0. */
-int kf_gemm_has_variant(int dtype, int block_m, int block_n, int block_k, int waves, int stages);
+/* 1 if (dtype, tile config, pipeline) has an instantiation in this build, else 0. */
+int kf_gemm_has_variant(int dtype, int block_m, int block_n, int block_k, int waves, int stages,
+                        int pipeline);
 
-/* Number of GEMM instantiations, and the tile config of instantiation `index`
- * (for the search space's "was it built" rule). Returns KF_OK or an error. */
+/* Number of GEMM instantiations (one per tile and pipeline), and the config of
+ * instantiation `index`. Returns KF_OK or an error. */
 int kf_gemm_variant_count(void);
 int kf_gemm_variant_info(int index, int* dtype, int* block_m, int* block_n, int* block_k,
-                         int* waves, int* stages);
+                         int* waves, int* stages, int* pipeline);
 
 /*
  * Split-K GEMV for decode shapes: y[M,N] = x[M,K] @ W[K,N], M <= 8.

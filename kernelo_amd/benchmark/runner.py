@@ -124,7 +124,7 @@ class CacheFlush:
         self._sink = torch.empty((), dtype=torch.float32, device=device)
 
     def flush(self) -> None:
-        torch.sum(self.buffer, dtype=torch.float32, out=self._sink)
+        torch.sum(self.buffer, dim=0, out=self._sink)
 
     # The reference zeroes its flush buffer with ``cache.zero_()``; keep that
     # spelling working for callers written against it.

@@ -55,8 +55,10 @@ TILES_PER_CHUNK = 8
 
 #: (dtype code, element bytes); codes match KF_DTYPE_* in include/kernelo_amd.h.
 DTYPES = ((0, 4), (1, 2), (2, 2))
-#: Loader pairs: 0 = VecK/VecN, 1 = VecK/VecK, 2 = Scalar/Scalar.
-COMBOS = (0, 1, 2)
+#: Loader pairs: 0 = VecK/VecN, 1 = VecK/VecK, 2 = Scalar/Scalar (register-staged
+#: pipeline); 3 = DMA with n-contiguous B, 4 = DMA with k-contiguous B (direct).
+COMBOS = (0, 1, 2, 3, 4)
+DIRECT_COMBOS = (3, 4)
 
 
 def generate() -> list[tuple[int, int, int, Path]]:
@@ -65,13 +67,14 @@ def generate() -> list[tuple[int, int, int, Path]]:
     from kernelo_amd.tuning.search import gemm_instantiations
 
     GEN.mkdir(parents=True, exist_ok=True)
-    tiles = gemm_instantiations()
+    staged = gemm_instantiations(direct=0)
+    direct = gemm_instantiations(direct=1)
     units = []
     registry = []
     for dt, elem in DTYPES:
-        lst = tiles[elem]
-        chunks = [lst[i : i + TILES_PER_CHUNK] for i in range(0, len(lst), TILES_PER_CHUNK)]
         for combo in COMBOS:
+            lst = (direct if combo in DIRECT_COMBOS else staged)[elem]
+            chunks = [lst[i : i + TILES_PER_CHUNK] for i in range(0, len(lst), TILES_PER_CHUNK)]
             for c, chunk in enumerate(chunks):
                 inc = GEN / f"gemm_tiles_{dt}_{combo}_{c}.inc"
                 inc.write_text("".join(f"KF_VARIANT({bm}, {bn}, {bk}, {w}, {s})\n" for bm, bn, bk, w, s in chunk))

@@ -130,9 +130,10 @@ struct VecKLoader {
   static constexpr int ITEMS = (ROWS * PER_ROW + NT - 1) / NT;
   u32x4 regs[ITEMS];
 
+  // FULL: the whole k-slice lies inside K (no masking in the steady state).
+  template <bool FULL>
   __device__ __forceinline__ void load(const T* base, int64_t ld_row, int64_t row0, int64_t nrows,
                                        int64_t k0, int64_t K, int tid) {
-    const bool full_k = (k0 + BK <= K);
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j) {
       const int item = tid + j * NT;
@@ -142,7 +143,7 @@ struct VecKLoader {
       int64_t row = row0 + r;
       row = row < nrows ? row : nrows - 1;
       const T* p = base + row * ld_row + k0 + kv * V;
-      if (full_k) {
+      if constexpr (FULL) {
         regs[j] = *reinterpret_cast<const u32x4*>(p);
       } else {
         T tmp[V];
@@ -175,6 +176,7 @@ struct ScalarLoader {
   static constexpr int ITEMS = (ROWS * PER_ROW + NT - 1) / NT;
   u32x4 regs[ITEMS];
 
+  template <bool FULL>
   __device__ __forceinline__ void load(const T* base, int64_t ld_row, int64_t ld_k, int64_t row0,
                                        int64_t nrows, int64_t k0, int64_t K, int tid) {
 #pragma unroll
@@ -189,7 +191,7 @@ struct ScalarLoader {
 #pragma unroll
       for (int e = 0; e < V; ++e) {
         const int64_t k = k0 + kv * V + e;
-        tmp[e] = (k < K) ? base[row * ld_row + k * ld_k] : static_cast<T>(0.f);
+        tmp[e] = (FULL || k < K) ? base[row * ld_row + k * ld_k] : static_cast<T>(0.f);
       }
       __builtin_memcpy(&regs[j], tmp, 16);
     }
@@ -219,9 +221,9 @@ struct VecNLoader {
   static constexpr int ITEMS = (SUBS + NT - 1) / NT;
   u32x4 regs[ITEMS][R];
 
+  template <bool FULL>
   __device__ __forceinline__ void load(const T* base, int64_t ldb_k, int64_t n0, int64_t N,
                                        int64_t k0, int64_t K, int tid) {
-    const bool full_k = (k0 + BK <= K);
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j) {
       const int item = tid + j * NT;
@@ -235,7 +237,7 @@ struct VecNLoader {
 #pragma unroll
       for (int q = 0; q < R; ++q) {
         const int64_t k = k0 + kr * R + q;
-        if (full_k || k < K)
+        if (FULL || k < K)
           regs[j][q] = *reinterpret_cast<const u32x4*>(base + k * ldb_k + col);
         else
           regs[j][q] = u32x4{0u, 0u, 0u, 0u};
@@ -315,18 +317,21 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(Args args) {
   ALd aload;
   BLd bload;
 
-  auto gload = [&](int64_t k0) {
+  auto gload = [&](int64_t k0, auto full_tag) {
+    constexpr bool F = decltype(full_tag)::value;
     if constexpr (ALOAD == kLoadScalar)
-      aload.load(A, args.lda_m, args.lda_k, m0, M, k0, K, tid);
+      aload.template load<F>(A, args.lda_m, args.lda_k, m0, M, k0, K, tid);
     else
-      aload.load(A, args.lda_m, m0, M, k0, K, tid);
+      aload.template load<F>(A, args.lda_m, m0, M, k0, K, tid);
     if constexpr (BLOAD == kLoadScalar)
-      bload.load(B, args.ldb_n, args.ldb_k, n0, N, k0, K, tid);
+      bload.template load<F>(B, args.ldb_n, args.ldb_k, n0, N, k0, K, tid);
     else if constexpr (BLOAD == kLoadVecN)
-      bload.load(B, args.ldb_k, n0, N, k0, K, tid);
+      bload.template load<F>(B, args.ldb_k, n0, N, k0, K, tid);
     else
-      bload.load(B, args.ldb_n, n0, N, k0, K, tid);
+      bload.template load<F>(B, args.ldb_n, n0, N, k0, K, tid);
   };
+  using Full = std::true_type;
+  using Part = std::false_type;
   auto sstore = [&](int stage) {
     T* As = smem + stage * (Tl::kLdsA + Tl::kLdsB);
     T* Bs = As + Tl::kLdsA;
@@ -367,16 +372,29 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(Args args) {
   };
 
   // ---- main loop: double-buffered LDS, one barrier per k-slice ----------
+  // The steady state only ever loads whole k-slices, so it has no masking and
+  // no data-dependent branches; the (at most one) partial slice at the end
+  // of K is peeled into the short loop after it.
   const int64_t nk = ceil_div(K, BK);
+  const int64_t nfull = K / BK;
   if (nk > 0) {
-    gload(0);
+    if (nfull > 0)
+      gload(0, Full{});
+    else
+      gload(0, Part{});
     sstore(0);
     __syncthreads();
-    for (int64_t kt = 0; kt < nk; ++kt) {
-      const int cur = static_cast<int>(kt & 1);
-      if (kt + 1 < nk) gload((kt + 1) * BK);
-      compute(cur);
-      if (kt + 1 < nk) sstore(cur ^ 1);
+    int64_t kt = 0;
+    for (; kt + 1 < nfull; ++kt) {
+      gload((kt + 1) * BK, Full{});
+      compute(static_cast<int>(kt & 1));
+      sstore(static_cast<int>((kt + 1) & 1));
+      __syncthreads();
+    }
+    for (; kt < nk; ++kt) {
+      if (kt + 1 < nk) gload((kt + 1) * BK, Part{});
+      compute(static_cast<int>(kt & 1));
+      if (kt + 1 < nk) sstore(static_cast<int>((kt + 1) & 1));
       __syncthreads();
     }
   }

@@ -50,7 +50,12 @@ __global__ __launch_bounds__(1024) void gemv_splitk(
   const int64_t kc = ceil_div(K, split_k);
   const int64_t kbeg = static_cast<int64_t>(s) * kc;
   const int64_t kend = (kbeg + kc < K) ? kbeg + kc : K;
-  const bool full = vec && (col0 + V <= N);
+  // With aligned rows and N a multiple of V every lane's vector is either
+  // wholly inside [0, N) or wholly past it. Lanes past N load a clamped,
+  // valid vector whose sums are never stored, so one branch-free loop serves
+  // every strip, including the last.
+  const bool vec_path = vec && (N % V == 0);
+  const int64_t col_ld = (col0 < N) ? col0 : N - V;
 
   float acc[MR][V];
 #pragma unroll
@@ -58,45 +63,62 @@ __global__ __launch_bounds__(1024) void gemv_splitk(
 #pragma unroll
     for (int e = 0; e < V; ++e) acc[m][e] = 0.f;
 
-  auto load_w = [&](int64_t k, float (&w)[V]) {
-    const T* row = W + k * ldw_k;
-    if (full) {
-      T tmp[V];
-      load16(row + col0, tmp);
+  // x rows past M read row M-1: their accumulators are never stored, and
+  // clamping keeps the loads unconditional.
+  const T* xrow[MR];
 #pragma unroll
-      for (int e = 0; e < V; ++e) w[e] = to_f32(tmp[e]);
-    } else {
+  for (int m = 0; m < MR; ++m) xrow[m] = x + ((m < M) ? m : M - 1) * ldx_m;
+
+  auto fma_row = [&](const float (&xv)[MR], const T (&w)[V]) {
 #pragma unroll
-      for (int e = 0; e < V; ++e) w[e] = (col0 + e < N) ? to_f32(row[(col0 + e) * ldw_n]) : 0.f;
-    }
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+      for (int e = 0; e < V; ++e) acc[m][e] = __builtin_fmaf(xv[m], to_f32(w[e]), acc[m][e]);
   };
 
   int64_t k = kbeg + wave;
-  // Main loop: kGemvUnroll rows per wave per trip, all loads issued first.
-  for (; k + static_cast<int64_t>(kGemvUnroll - 1) * nwaves < kend;
-       k += static_cast<int64_t>(kGemvUnroll) * nwaves) {
-    float w[kGemvUnroll][V];
+  const int64_t step = nwaves;
+  if (vec_path) {
+    const T* wcol = W + col_ld;
+    // kGemvUnroll rows per wave per trip. The x values go first so that the
+    // wait for them does not also wait for the W rows behind them; then all
+    // W loads issue back to back and are consumed in order.
+    for (; k + (kGemvUnroll - 1) * step < kend; k += kGemvUnroll * step) {
+      float xv[kGemvUnroll][MR];
 #pragma unroll
-    for (int u = 0; u < kGemvUnroll; ++u) load_w(k + static_cast<int64_t>(u) * nwaves, w[u]);
+      for (int u = 0; u < kGemvUnroll; ++u)
 #pragma unroll
-    for (int u = 0; u < kGemvUnroll; ++u) {
-      const int64_t kk = k + static_cast<int64_t>(u) * nwaves;
+        for (int m = 0; m < MR; ++m) xv[u][m] = to_f32(xrow[m][(k + u * step) * ldx_k]);
+      u32x4 raw[kGemvUnroll];
 #pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        const float xv = (m < M) ? to_f32(x[m * ldx_m + kk * ldx_k]) : 0.f;
+      for (int u = 0; u < kGemvUnroll; ++u)
+        raw[u] = *reinterpret_cast<const u32x4*>(wcol + (k + u * step) * ldw_k);
 #pragma unroll
-        for (int e = 0; e < V; ++e) acc[m][e] = __builtin_fmaf(xv, w[u][e], acc[m][e]);
+      for (int u = 0; u < kGemvUnroll; ++u) {
+        T w[V];
+        __builtin_memcpy(w, &raw[u], 16);
+        fma_row(xv[u], w);
       }
     }
-  }
-  for (; k < kend; k += nwaves) {
-    float w[V];
-    load_w(k, w);
+    for (; k < kend; k += step) {
+      float xv[MR];
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      const float xv = (m < M) ? to_f32(x[m * ldx_m + k * ldx_k]) : 0.f;
+      for (int m = 0; m < MR; ++m) xv[m] = to_f32(xrow[m][k * ldx_k]);
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(wcol + k * ldw_k);
+      T w[V];
+      __builtin_memcpy(w, &raw, 16);
+      fma_row(xv, w);
+    }
+  } else {
+    for (; k < kend; k += step) {
+      float xv[MR];
 #pragma unroll
-      for (int e = 0; e < V; ++e) acc[m][e] = __builtin_fmaf(xv, w[e], acc[m][e]);
+      for (int m = 0; m < MR; ++m) xv[m] = to_f32(xrow[m][k * ldx_k]);
+      T w[V];
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        w[e] = (col0 + e < N) ? W[k * ldw_k + (col0 + e) * ldw_n] : from_f32<T>(0.f);
+      fma_row(xv, w);
     }
   }
 
@@ -118,32 +140,62 @@ __global__ __launch_bounds__(1024) void gemv_splitk(
 
   if (split_k > 1) {
     // Publish this slice's partial sums, then take a ticket for the strip.
+    // The partials move through agent-scope relaxed atomic stores/loads,
+    // which are coherent across XCDs without writing back or invalidating
+    // whole L2s (what a device-scope fence costs here); the only ordering
+    // needed is that the stores have completed before the ticket is taken.
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       if (m >= M) break;
       float* dst = ws + (static_cast<int64_t>(s) * M + m) * N;
 #pragma unroll
       for (int e = 0; e < V; ++e)
-        if (col0 + e < N) dst[col0 + e] = acc[m][e];
+        if (col0 + e < N)
+          __hip_atomic_store(dst + col0 + e, acc[m][e], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
     }
-    __threadfence();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the partial stores are done
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     unsigned ticket = 0;
-    if (lane == 0) ticket = atomicAdd(&tickets[nb], 1u);
+    if (lane == 0)
+      ticket = __hip_atomic_fetch_add(&tickets[nb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     ticket = __shfl(ticket, 0, kWave);
     if (ticket != static_cast<unsigned>(split_k - 1)) return;
-    __threadfence();
+    // Sum the slices in ascending order (deterministic). kSliceBatch slices'
+    // loads are issued before any is added, so they are in flight together.
+    constexpr int kSliceBatch = 4;
+    const int64_t cl = (col0 < N) ? col0 : N - 1;  // lanes past N read a valid column
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       if (m >= M) break;
+      float r[V];
 #pragma unroll
-      for (int e = 0; e < V; ++e) {
-        float r = 0.f;
-        if (col0 + e < N)
-          for (int q = 0; q < split_k; ++q) r += ws[(static_cast<int64_t>(q) * M + m) * N + col0 + e];
-        acc[m][e] = r;
+      for (int e = 0; e < V; ++e) r[e] = 0.f;
+      const float* src = ws + static_cast<int64_t>(m) * N;
+      for (int q0 = 0; q0 < split_k; q0 += kSliceBatch) {
+        float part[kSliceBatch][V];
+#pragma unroll
+        for (int b = 0; b < kSliceBatch; ++b) {
+          const int q = (q0 + b < split_k) ? q0 + b : split_k - 1;
+#pragma unroll
+          for (int e = 0; e < V; ++e) {
+            const int64_t c = (cl + e < N) ? cl + e : N - 1;
+            part[b][e] = __hip_atomic_load(src + static_cast<int64_t>(q) * M * N + c,
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+#pragma unroll
+        for (int b = 0; b < kSliceBatch; ++b)
+          if (q0 + b < split_k)
+#pragma unroll
+            for (int e = 0; e < V; ++e) r[e] += part[b][e];
       }
+#pragma unroll
+      for (int e = 0; e < V; ++e) acc[m][e] = r[e];
     }
-    if (lane == 0) tickets[nb] = 0u;  // ready for the next launch
+    if (lane == 0)
+      __hip_atomic_store(&tickets[nb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
 #pragma unroll

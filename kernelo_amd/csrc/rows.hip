@@ -24,39 +24,77 @@ template <typename T, int EPT>
 struct RowTile {
   static constexpr int V = (EPT < Vec<T>::N) ? EPT : Vec<T>::N;
   static constexpr int NV = EPT / V;
+  static constexpr bool kVector = (V == Vec<T>::N);
   float v[EPT];
+
+  // Vector path: aligned rows whose width is a multiple of V. Then every
+  // lane's slot is wholly inside the row or wholly past it; lanes past the
+  // row load a clamped valid vector and substitute `fill`, so all loads
+  // issue back to back with no per-lane branches.
+  __device__ __forceinline__ static bool vector_ok(bool vec, int64_t cols) {
+    return kVector && vec && cols >= V && cols % V == 0;
+  }
 
   __device__ __forceinline__ void load(const T* row, int64_t cols, int t, int nt, bool vec,
                                        float fill) {
+    if constexpr (kVector) {
+      if (vector_ok(vec, cols)) {
+        load_vector(row, cols, t, nt, fill);
+        return;
+      }
+    }
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int64_t c0 = (static_cast<int64_t>(j) * nt + t) * V;
-      if (vec && V == Vec<T>::N && c0 + V <= cols) {
-        T tmp[Vec<T>::N];
-        load16(row + c0, tmp);
 #pragma unroll
-        for (int e = 0; e < V; ++e) v[j * V + e] = to_f32(tmp[e]);
-      } else {
+      for (int e = 0; e < V; ++e) v[j * V + e] = (c0 + e < cols) ? to_f32(row[c0 + e]) : fill;
+    }
+  }
+
+  __device__ __forceinline__ void load_vector(const T* row, int64_t cols, int t, int nt,
+                                              float fill) {
+    {
+      u32x4 raw[NV];
 #pragma unroll
-        for (int e = 0; e < V; ++e) v[j * V + e] = (c0 + e < cols) ? to_f32(row[c0 + e]) : fill;
+      for (int j = 0; j < NV; ++j) {
+        const int64_t c0 = (static_cast<int64_t>(j) * nt + t) * V;
+        raw[j] = *reinterpret_cast<const u32x4*>(row + ((c0 < cols) ? c0 : cols - V));
+      }
+      // Convert only after every load has been issued.
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int64_t c0 = (static_cast<int64_t>(j) * nt + t) * V;
+        T tmp[V];
+        __builtin_memcpy(tmp, &raw[j], 16);
+#pragma unroll
+        for (int e = 0; e < V; ++e) v[j * V + e] = (c0 < cols) ? to_f32(tmp[e]) : fill;
       }
     }
   }
 
   template <typename F>
   __device__ __forceinline__ void store(T* row, int64_t cols, int t, int nt, bool vec, F f) const {
+    const bool vpath = vector_ok(vec, cols);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int64_t c0 = (static_cast<int64_t>(j) * nt + t) * V;
-      if (vec && V == Vec<T>::N && c0 + V <= cols) {
-        T tmp[Vec<T>::N];
+      T tmp[V];
 #pragma unroll
-        for (int e = 0; e < V; ++e) tmp[e] = from_f32<T>(f(v[j * V + e], j * V + e));
-        store16(row + c0, tmp);
-      } else {
+      for (int e = 0; e < V; ++e) tmp[e] = from_f32<T>(f(v[j * V + e], j * V + e));
+      if constexpr (kVector) {
+        if (vpath) {
+          if (c0 < cols) {
+            u32x4 raw;
+            __builtin_memcpy(&raw, tmp, 16);
+            *reinterpret_cast<u32x4*>(row + c0) = raw;
+          }
+          continue;
+        }
+      }
+      {
 #pragma unroll
         for (int e = 0; e < V; ++e)
-          if (c0 + e < cols) row[c0 + e] = from_f32<T>(f(v[j * V + e], j * V + e));
+          if (c0 + e < cols) row[c0 + e] = tmp[e];
       }
     }
   }

@@ -66,7 +66,8 @@ def linear_gelu_reference(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor) 
 class FusedLinearOperator(Operator):
     name = "fused_linear"
     config_order = (
-        "BLOCK_M", "BLOCK_N", "BLOCK_K", "GROUP_M", "GEMV", "SPLIT_K", "num_warps", "num_stages",
+        "BLOCK_M", "BLOCK_N", "BLOCK_K", "GROUP_M", "DIRECT", "GEMV", "SPLIT_K", "num_warps",
+        "num_stages",
     )
 
     def search_space(self) -> FusedLinearSearchSpace:

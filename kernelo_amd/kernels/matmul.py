@@ -87,7 +87,8 @@ def launch_gemm(
         m, n, k, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
         out.stride(0), out.stride(1), epilogue,
         cfg["BLOCK_M"], cfg["BLOCK_N"], cfg["BLOCK_K"], cfg["num_warps"],
-        cfg.get("num_stages", 2), cfg.get("GROUP_M", 8), stream,
+        cfg.get("num_stages", 2), cfg.get("GROUP_M", 8),
+        hip.KF_PIPELINE_DIRECT if cfg.get("DIRECT") else hip.KF_PIPELINE_STAGED, stream,
     )
     hip.check(rc, "gemm")
     return out
@@ -105,7 +106,8 @@ def matmul(a: torch.Tensor, b: torch.Tensor, *, config: KernelConfig | None = No
 class MatmulOperator(Operator):
     name = "matmul"
     config_order = (
-        "BLOCK_M", "BLOCK_N", "BLOCK_K", "GROUP_M", "GEMV", "SPLIT_K", "num_warps", "num_stages",
+        "BLOCK_M", "BLOCK_N", "BLOCK_K", "GROUP_M", "DIRECT", "GEMV", "SPLIT_K", "num_warps",
+        "num_stages",
     )
 
     def search_space(self) -> MatmulSearchSpace:

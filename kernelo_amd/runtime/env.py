@@ -142,9 +142,15 @@ def device_caps(device: torch.device | str | int | None = None) -> DeviceCaps:
             peak_fp32_tflops=0.0,
             peak_hbm_gbps=0.0,
         )
+    # Without libdrm's marketing-name table the runtime reports a generic
+    # "AMD Radeon Graphics"; a known architecture with the table's CU count
+    # is that board, and the cache key must not depend on the host's libdrm.
+    name = props.name or base.name
+    if "Instinct" not in name and int(props.multi_processor_count) == base.cu_count:
+        name = base.name
     return replace(
         base,
-        name=props.name or base.name,
+        name=name,
         gcn_arch=arch,
         total_memory_bytes=int(props.total_memory),
         cu_count=int(props.multi_processor_count) or base.cu_count,

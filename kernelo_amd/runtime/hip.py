@@ -33,6 +33,9 @@ KF_ERR_OUT_OF_MEMORY = -7
 KF_EPILOGUE_NONE = 0
 KF_EPILOGUE_BIAS_GELU = 1
 
+KF_PIPELINE_STAGED = 0
+KF_PIPELINE_DIRECT = 1
+
 
 class KernelError(RuntimeError):
     """A status code other than KF_OK from the C-ABI."""
@@ -95,13 +98,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "kf_gemm": (
         _int,
         [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int,
-         _int, _int, _int, _int, _int, _int, _vp],
+         _int, _int, _int, _int, _int, _int, _int, _vp],
     ),
-    "kf_gemm_has_variant": (_int, [_int, _int, _int, _int, _int, _int]),
+    "kf_gemm_has_variant": (_int, [_int, _int, _int, _int, _int, _int, _int]),
     "kf_gemm_variant_count": (_int, []),
     "kf_gemm_variant_info": (
         _int,
-        [_int] + [ctypes.POINTER(_int)] * 6,
+        [_int] + [ctypes.POINTER(_int)] * 7,
     ),
     "kf_gemv": (
         _int,
@@ -181,11 +184,11 @@ def require_device_tensor(*tensors: torch.Tensor) -> None:
             raise ValueError(f"operands on different devices: {dev} vs {t.device}")
 
 
-def gemm_variants() -> list[tuple[int, int, int, int, int, int]]:
-    """(dtype code, BLOCK_M, BLOCK_N, BLOCK_K, waves, stages) for every compiled tile."""
+def gemm_variants() -> list[tuple[int, int, int, int, int, int, int]]:
+    """(dtype code, BLOCK_M, BLOCK_N, BLOCK_K, waves, stages, pipeline) per compiled tile."""
     lib = load()
     out = []
-    vals = [_int() for _ in range(6)]
+    vals = [_int() for _ in range(7)]
     for i in range(lib.kf_gemm_variant_count()):
         check(lib.kf_gemm_variant_info(i, *[ctypes.byref(v) for v in vals]), "gemm variant info")
         out.append(tuple(v.value for v in vals))

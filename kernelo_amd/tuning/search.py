@@ -159,7 +159,11 @@ class SearchSpace(ABC):
         floor = caps.cu_count // 2
         kept = [c for c in configs if programs[c] >= floor]
         dropped = [
-            (c, f"launch grid of {programs[c]} workgroups fills under half of {caps.cu_count} CUs")
+            (
+                c,
+                f"underfilled: launch grid of {programs[c]} workgroups fills under half of "
+                f"{caps.cu_count} CUs",
+            )
             for c in configs
             if programs[c] < floor
         ]
@@ -252,20 +256,67 @@ def gemm_lds_bytes(block_m: int, block_n: int, block_k: int, stages: int, elem: 
     return stages * (block_m + block_n) * (block_k + pad) * elem
 
 
-def gemm_tile_regs(block_m: int, block_n: int, block_k: int, waves: int, elem: int) -> dict[str, int]:
-    """Per-lane register model of one tile: accumulators, fragments, staged loads."""
+def gemm_tile_regs(
+    block_m: int, block_n: int, block_k: int, waves: int, elem: int, *, direct: int = 0
+) -> dict[str, int]:
+    """Per-lane register model of one tile: accumulators, fragments, staged loads.
+
+    The direct pipeline stages nothing in registers (the DMA writes LDS).
+    """
     lanes = waves * 64
     wm, wn = wave_grid(waves, block_m, block_n)
     acc = block_m * block_n // lanes
     frags = 4 * (block_m // wm // MFMA_TILE + block_n // wn // MFMA_TILE)
-    staged = 4 * ceil_div((block_m + block_n) * block_k * elem, VECTOR_BYTES * lanes)
+    staged = 0 if direct else 4 * ceil_div((block_m + block_n) * block_k * elem, VECTOR_BYTES * lanes)
     return {"acc": acc, "frags": frags, "staged": staged, "total": acc + frags + staged}
 
 
-def gemm_instantiation_reason(
+#: The direct-to-LDS pipeline moves one 128-byte A row segment per k-slice.
+DIRECT_BLOCK_K = 64
+
+
+def gemm_direct_lds_bytes(block_m: int, block_n: int, stages: int) -> int:
+    """LDS of the direct pipeline: dense (unpadded, swizzled) 16-bit stages."""
+    return stages * (block_m + block_n) * DIRECT_BLOCK_K * 2
+
+
+def gemm_direct_reason(
     block_m: int, block_n: int, block_k: int, waves: int, stages: int, elem: int, caps: DeviceCaps
 ) -> str | None:
+    """Extra shape-independent rules of the direct (global->LDS DMA) pipeline."""
+    if elem != 2:
+        return "direct DMA: 16-bit inputs only (the transposing LDS read is b16)"
+    if block_k != DIRECT_BLOCK_K:
+        return f"direct DMA: BLOCK_K must be {DIRECT_BLOCK_K} (one 128-byte A row per slice)"
+    lanes = waves * 64
+    if (block_m * DIRECT_BLOCK_K // 8) % lanes or (block_n * DIRECT_BLOCK_K // 8) % lanes:
+        return f"direct DMA: {block_m}x{block_n} slices do not split into whole 16-byte chunks per lane"
+    if block_n < 64:
+        return f"direct DMA: BLOCK_N={block_n} leaves too few chunks per row for the bank swizzle"
+    lds = gemm_direct_lds_bytes(block_m, block_n, stages)
+    if lds > caps.lds_per_workgroup:
+        return (
+            f"LDS: {lds // 1024} KiB of A/B stages exceeds the "
+            f"{caps.lds_per_workgroup // 1024} KiB per-workgroup limit"
+        )
+    return None
+
+
+def gemm_instantiation_reason(
+    block_m: int,
+    block_n: int,
+    block_k: int,
+    waves: int,
+    stages: int,
+    elem: int,
+    caps: DeviceCaps,
+    direct: int = 0,
+) -> str | None:
     """Shape-independent rules: why this tile is not compiled, or ``None``."""
+    if direct:
+        reason = gemm_direct_reason(block_m, block_n, block_k, waves, stages, elem, caps)
+        if reason is not None:
+            return reason
     kstep = MFMA_K[elem]
     if block_k % kstep:
         return f"MFMA k step: BLOCK_K={block_k} is not a multiple of {kstep} for {elem}-byte inputs"
@@ -276,12 +327,12 @@ def gemm_instantiation_reason(
             f"{MFMA_TILE}x{MFMA_TILE} MFMA fragments"
         )
     lds = gemm_lds_bytes(block_m, block_n, block_k, stages, elem)
-    if lds > caps.lds_per_workgroup:
+    if not direct and lds > caps.lds_per_workgroup:
         return (
             f"LDS: {lds // 1024} KiB of A/B stages exceeds the "
             f"{caps.lds_per_workgroup // 1024} KiB per-workgroup limit"
         )
-    regs = gemm_tile_regs(block_m, block_n, block_k, waves, elem)
+    regs = gemm_tile_regs(block_m, block_n, block_k, waves, elem, direct=direct)
     if regs["acc"] > MAX_ACC_REGS_PER_LANE:
         return f"register pressure: {regs['acc']} accumulator registers per lane"
     if regs["total"] > MAX_TILE_REGS_PER_LANE:
@@ -297,6 +348,8 @@ class _GemmSpace(SearchSpace):
     BLOCK_K = (16, 32, 64)
     NUM_WARPS = (4, 8)
     NUM_STAGES = (2,)
+    #: 0: register-staged LDS pipeline; 1: global->LDS DMA pipeline.
+    DIRECT = (0, 1)
     GROUP_M = 8
 
     #: Split-K GEMV grid, offered when M is at most GEMV_MAX_M.
@@ -309,8 +362,8 @@ class _GemmSpace(SearchSpace):
     GEMV_MAX_LDS = 64 * 1024
 
     def grid(self, problem: Problem) -> Iterator[KernelConfig]:
-        for bm, bn, bk, warps, stages in product(
-            self.BLOCK_M, self.BLOCK_N, self.BLOCK_K, self.NUM_WARPS, self.NUM_STAGES
+        for direct, bm, bn, bk, warps, stages in product(
+            self.DIRECT, self.BLOCK_M, self.BLOCK_N, self.BLOCK_K, self.NUM_WARPS, self.NUM_STAGES
         ):
             yield KernelConfig(
                 self.operation,
@@ -318,6 +371,7 @@ class _GemmSpace(SearchSpace):
                 BLOCK_N=bn,
                 BLOCK_K=bk,
                 GROUP_M=self.GROUP_M,
+                DIRECT=direct,
                 num_warps=warps,
                 num_stages=stages,
             )
@@ -341,7 +395,14 @@ class _GemmSpace(SearchSpace):
 
         bm, bn = config["BLOCK_M"], config["BLOCK_N"]
         reason = gemm_instantiation_reason(
-            bm, bn, config["BLOCK_K"], config["num_warps"], config["num_stages"], elem, caps
+            bm,
+            bn,
+            config["BLOCK_K"],
+            config["num_warps"],
+            config["num_stages"],
+            elem,
+            caps,
+            direct=config.get("DIRECT", 0),
         )
         if reason is not None:
             return reason
@@ -398,7 +459,14 @@ class _GemmSpace(SearchSpace):
         reuse = (bm * bn) / (bm + bn)
         padded = ceil_div(dims["M"], bm) * bm * ceil_div(dims["N"], bn) * bn
         waste = padded / (dims["M"] * dims["N"])
-        return (1, -min(programs, caps.cu_count), -reuse, waste, config["num_warps"])
+        return (
+            1,
+            -min(programs, caps.cu_count),
+            -reuse,
+            waste,
+            -config.get("DIRECT", 0),
+            config["num_warps"],
+        )
 
 
 class MatmulSearchSpace(_GemmSpace):
@@ -409,8 +477,10 @@ class FusedLinearSearchSpace(_GemmSpace):
     operation = "fused_linear"
 
 
-def gemm_instantiations(caps: DeviceCaps | None = None) -> dict[int, list[tuple[int, ...]]]:
-    """Tile configs the build compiles, keyed by element size in bytes.
+def gemm_instantiations(
+    caps: DeviceCaps | None = None, *, direct: int = 0
+) -> dict[int, list[tuple[int, ...]]]:
+    """Tile configs the build compiles for one pipeline, keyed by element size.
 
     Every (BLOCK_M, BLOCK_N, BLOCK_K, num_warps, num_stages) point of the
     GEMM grid that passes the shape-independent rules.
@@ -426,7 +496,7 @@ def gemm_instantiations(caps: DeviceCaps | None = None) -> dict[int, list[tuple[
             for bm, bn, bk, w, s in product(
                 space.BLOCK_M, space.BLOCK_N, space.BLOCK_K, space.NUM_WARPS, space.NUM_STAGES
             )
-            if gemm_instantiation_reason(bm, bn, bk, w, s, elem, caps) is None
+            if gemm_instantiation_reason(bm, bn, bk, w, s, elem, caps, direct=direct) is None
         ]
     return out
 

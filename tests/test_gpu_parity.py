@@ -150,25 +150,35 @@ def test_matmul_correctness_suite(m, n, k, dtype):
 
 
 _TILES = [
-    (32, 32, 32, 4),
-    (64, 64, 64, 4),
-    (128, 128, 64, 4),
-    (256, 128, 64, 4),
-    (128, 256, 32, 8),
-    (256, 256, 64, 8),
-    (64, 256, 64, 8),
+    (32, 32, 32, 4, 0),
+    (64, 64, 64, 4, 0),
+    (128, 128, 64, 4, 0),
+    (256, 128, 64, 4, 0),
+    (128, 256, 32, 8, 0),
+    (256, 256, 64, 8, 0),
+    (64, 256, 64, 8, 0),
+    (64, 64, 64, 4, 1),
+    (128, 128, 64, 4, 1),
+    (128, 128, 64, 8, 1),
+    (256, 128, 64, 8, 1),
+    (256, 256, 64, 8, 1),
+    (128, 256, 64, 4, 1),
 ]
 
 
 @pytest.mark.parametrize("tile", _TILES, ids=lambda t: "x".join(map(str, t)))
 @pytest.mark.parametrize("layout", ("nn", "nt", "tn"))
-@pytest.mark.parametrize("m,n,k", [(257, 513, 129), (1023, 4097, 127), (512, 512, 512)])
-def test_matmul_tiles_and_layouts(tile, layout, m, n, k):
-    """Every loader pair: row-major B (VecN), transposed B (VecK), strided A (scalar)."""
+@pytest.mark.parametrize(
+    "m,n,k", [(257, 513, 129), (1023, 4097, 127), (512, 512, 512), (300, 520, 136), (64, 64, 8)]
+)
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16), ids=("fp16", "bf16"))
+def test_matmul_tiles_and_layouts(tile, layout, m, n, k, dtype):
+    """Every loader pair and pipeline: row-major B (VecN / DMA + transposing
+    reads), transposed B (VecK / DMA), strided A (scalar); K tails that are and
+    are not multiples of 8 (the DMA path zeroes chunks past K)."""
     from kernelo_amd.kernels.matmul import matmul
 
-    bm, bn, bk, w = tile
-    dtype = torch.float16
+    bm, bn, bk, w, direct = tile
     a = _randn(m, k, dtype=dtype, seed=1)
     b = _randn(k, n, dtype=dtype, seed=2)
     da, db = a.to(DEV), b.to(DEV)
@@ -177,7 +187,8 @@ def test_matmul_tiles_and_layouts(tile, layout, m, n, k):
     if layout[0] == "t":
         da = a.t().contiguous().to(DEV).t()
     cfg = KernelConfig(
-        "matmul", BLOCK_M=bm, BLOCK_N=bn, BLOCK_K=bk, GROUP_M=8, num_warps=w, num_stages=2
+        "matmul", BLOCK_M=bm, BLOCK_N=bn, BLOCK_K=bk, GROUP_M=8, DIRECT=direct, num_warps=w,
+        num_stages=2,
     )
     out = matmul(da, db, config=cfg)
     _gate(ops.matmul_ref(a, b), out, dtype, f"{cfg} {layout} {m}x{n}x{k}")
@@ -316,7 +327,7 @@ def _guarded_call(m, n, k, cfg, seed, dtype=torch.bfloat16):
         rc = lib.kf_gemm(abi_code(dtype), da.data_ptr(), db.data_ptr(), None, cptr, m, n, k,
                          da.stride(0), da.stride(1), db.stride(0), db.stride(1), pitch, 1, 0,
                          cfg["BLOCK_M"], cfg["BLOCK_N"], cfg["BLOCK_K"], cfg["num_warps"], 2, 8,
-                         stream)
+                         int(cfg.get("DIRECT", 0)), stream)
     hip.check(rc, "guarded call")
     torch.cuda.synchronize()
     host = buf.cpu().view(m + 2 * pad, pitch).float()
@@ -332,6 +343,8 @@ def _guarded_call(m, n, k, cfg, seed, dtype=torch.bfloat16):
         (1023, 4097, 127, KernelConfig("matmul", BLOCK_M=128, BLOCK_N=128, BLOCK_K=32, GROUP_M=8, num_warps=4, num_stages=2)),
         (1023, 4097, 127, KernelConfig("matmul", BLOCK_M=256, BLOCK_N=128, BLOCK_K=64, GROUP_M=8, num_warps=4, num_stages=2)),
         (1023, 4097, 127, KernelConfig("matmul", BLOCK_M=32, BLOCK_N=64, BLOCK_K=32, GROUP_M=8, num_warps=4, num_stages=2)),
+        (1023, 4096, 136, KernelConfig("matmul", BLOCK_M=128, BLOCK_N=128, BLOCK_K=64, GROUP_M=8, DIRECT=1, num_warps=4, num_stages=2)),
+        (1000, 1032, 72, KernelConfig("matmul", BLOCK_M=256, BLOCK_N=256, BLOCK_K=64, GROUP_M=8, DIRECT=1, num_warps=8, num_stages=2)),
         (1, 7, 3, KernelConfig("matmul", GEMV=1, SPLIT_K=1, num_warps=1)),
         (1, 7, 3, KernelConfig("matmul", GEMV=1, SPLIT_K=2, num_warps=4)),
         (1, 7, 3, KernelConfig("matmul", BLOCK_M=32, BLOCK_N=32, BLOCK_K=32, GROUP_M=8, num_warps=4, num_stages=2)),
