@@ -168,43 +168,40 @@ struct VecKLoader {
 };
 
 // A or B with element loads at arbitrary strides (misaligned rows, views).
-// Element (row, k) lives at base + row*ld_row + k*ld_k.
+// Element (row, k) lives at base + row*ld_row + k*ld_k. The layouts it serves
+// are the slow fallback, so it trades overlap for registers: load_to_lds()
+// writes each 16-byte LDS chunk as soon as its elements arrive (the next
+// stage is free while the current one is multiplied) and keeps nothing live
+// across the compute.
 template <typename T, int ROWS, int BK, int NT>
 struct ScalarLoader {
   static constexpr int V = Vec<T>::N;
   static constexpr int PER_ROW = BK / V;
   static constexpr int ITEMS = (ROWS * PER_ROW + NT - 1) / NT;
-  u32x4 regs[ITEMS];
 
   template <bool FULL>
-  __device__ __forceinline__ void load(const T* base, int64_t ld_row, int64_t ld_k, int64_t row0,
-                                       int64_t nrows, int64_t k0, int64_t K, int tid) {
-#pragma unroll
+  __device__ __forceinline__ void load_to_lds(T* lds, const T* base, int64_t ld_row, int64_t ld_k,
+                                              int64_t row0, int64_t nrows, int64_t k0, int64_t K,
+                                              int tid) const {
+#pragma unroll 1
     for (int j = 0; j < ITEMS; ++j) {
       const int item = tid + j * NT;
-      if ((ROWS * PER_ROW) % NT != 0 && item >= ROWS * PER_ROW) break;
+      if (item >= ROWS * PER_ROW) break;
       const int r = item / PER_ROW;
       const int kv = item % PER_ROW;
       int64_t row = row0 + r;
       row = row < nrows ? row : nrows - 1;
+      const int64_t kb = k0 + kv * V;
+      const T* p = base + row * ld_row + kb * ld_k;
       T tmp[V];
 #pragma unroll
       for (int e = 0; e < V; ++e) {
-        const int64_t k = k0 + kv * V + e;
-        tmp[e] = (FULL || k < K) ? base[row * ld_row + k * ld_k] : static_cast<T>(0.f);
+        tmp[e] = (FULL || kb + e < K) ? *p : static_cast<T>(0.f);
+        p += ld_k;
       }
-      __builtin_memcpy(&regs[j], tmp, 16);
-    }
-  }
-
-  __device__ __forceinline__ void store(T* lds, int tid) const {
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
-      const int item = tid + j * NT;
-      if ((ROWS * PER_ROW) % NT != 0 && item >= ROWS * PER_ROW) break;
-      const int r = item / PER_ROW;
-      const int kv = item % PER_ROW;
-      *reinterpret_cast<u32x4*>(lds + r * (BK + V) + kv * V) = regs[j];
+      u32x4 raw;
+      __builtin_memcpy(&raw, tmp, 16);
+      *reinterpret_cast<u32x4*>(lds + r * (BK + V) + kv * V) = raw;
     }
   }
 };
@@ -317,26 +314,35 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(Args args) {
   ALd aload;
   BLd bload;
 
-  auto gload = [&](int64_t k0, auto full_tag) {
+  // Fetch k-slice k0 for LDS stage `stage`: vector loaders stage it in
+  // registers (written by sstore after the compute), the scalar loader writes
+  // the stage directly.
+  auto gload = [&](int64_t k0, auto full_tag, int stage) {
     constexpr bool F = decltype(full_tag)::value;
+    T* As = smem + stage * (Tl::kLdsA + Tl::kLdsB);
+    T* Bs = As + Tl::kLdsA;
     if constexpr (ALOAD == kLoadScalar)
-      aload.template load<F>(A, args.lda_m, args.lda_k, m0, M, k0, K, tid);
+      aload.template load_to_lds<F>(As, A, args.lda_m, args.lda_k, m0, M, k0, K, tid);
     else
       aload.template load<F>(A, args.lda_m, m0, M, k0, K, tid);
     if constexpr (BLOAD == kLoadScalar)
-      bload.template load<F>(B, args.ldb_n, args.ldb_k, n0, N, k0, K, tid);
+      bload.template load_to_lds<F>(Bs, B, args.ldb_n, args.ldb_k, n0, N, k0, K, tid);
     else if constexpr (BLOAD == kLoadVecN)
       bload.template load<F>(B, args.ldb_k, n0, N, k0, K, tid);
     else
       bload.template load<F>(B, args.ldb_n, n0, N, k0, K, tid);
+    (void)As;
+    (void)Bs;
   };
   using Full = std::true_type;
   using Part = std::false_type;
   auto sstore = [&](int stage) {
     T* As = smem + stage * (Tl::kLdsA + Tl::kLdsB);
     T* Bs = As + Tl::kLdsA;
-    aload.store(As, tid);
-    bload.store(Bs, tid);
+    if constexpr (ALOAD != kLoadScalar) aload.store(As, tid);
+    if constexpr (BLOAD != kLoadScalar) bload.store(Bs, tid);
+    (void)As;
+    (void)Bs;
   };
 
   f32x4 acc[FM][FN];
@@ -379,20 +385,20 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(Args args) {
   const int64_t nfull = K / BK;
   if (nk > 0) {
     if (nfull > 0)
-      gload(0, Full{});
+      gload(0, Full{}, 0);
     else
-      gload(0, Part{});
+      gload(0, Part{}, 0);
     sstore(0);
     __syncthreads();
     int64_t kt = 0;
     for (; kt + 1 < nfull; ++kt) {
-      gload((kt + 1) * BK, Full{});
+      gload((kt + 1) * BK, Full{}, static_cast<int>((kt + 1) & 1));
       compute(static_cast<int>(kt & 1));
       sstore(static_cast<int>((kt + 1) & 1));
       __syncthreads();
     }
     for (; kt < nk; ++kt) {
-      if (kt + 1 < nk) gload((kt + 1) * BK, Part{});
+      if (kt + 1 < nk) gload((kt + 1) * BK, Part{}, static_cast<int>((kt + 1) & 1));
       compute(static_cast<int>(kt & 1));
       if (kt + 1 < nk) sstore(static_cast<int>((kt + 1) & 1));
       __syncthreads();

@@ -30,8 +30,13 @@ __device__ __forceinline__ float gelu_tanh(float a) {
   return a / (1.0f + __builtin_amdgcn_exp2f(-inner * kLog2e));
 }
 
+// Eight x rows need 8x the accumulators and x values: cap the workgroup at
+// 512 lanes so each lane may use 256 registers.
+template <int MR>
+constexpr int gemv_max_lanes() { return MR > 4 ? 512 : 1024; }
+
 template <typename T, int MR>
-__global__ __launch_bounds__(1024) void gemv_splitk(
+__global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_splitk(
     const T* __restrict__ x, const T* __restrict__ W, const T* __restrict__ bias,
     T* __restrict__ y, int64_t M, int64_t N, int64_t K, int64_t ldx_m, int64_t ldx_k,
     int64_t ldw_k, int64_t ldw_n, int64_t ldy_m, int64_t ldy_n, int epilogue, int split_k,
@@ -230,6 +235,11 @@ int launch_gemv(const void* x, const void* W, const void* bias, void* y, int64_t
   float* partial = ws ? reinterpret_cast<float*>(static_cast<char*>(ws) + ticket_bytes(N)) : nullptr;
   auto go = [&](auto mr) -> int {
     constexpr int MR = decltype(mr)::value;
+    if (waves * kWave > gemv_max_lanes<MR>()) {
+      set_error("gemv: register pressure: %d rows allow at most %d waves, got %d", MR,
+                gemv_max_lanes<MR>() / kWave, waves);
+      return KF_ERR_OUT_OF_RESOURCES;
+    }
     const size_t lds = static_cast<size_t>(waves) * MR * kWave * V * sizeof(float);
     if (lds > kGemvMaxLds) {
       set_error("gemv: waves=%d x %d rows needs %zu B of LDS for the wave reduction (limit %zu)",

@@ -15,6 +15,13 @@ namespace kf {
 namespace {
 
 constexpr int kMaxWaves = 16;  // 1024 lanes, the workgroup limit
+// A workgroup keeps at most 16384 fp32 row values in registers (64 KiB): the
+// single-pass limit. EPT values per lane therefore allow 16384/EPT lanes, and
+// the launch bound tells the compiler that, so it can give each lane the
+// registers EPT (and RMSNorm's gamma copy) need without spilling.
+constexpr int kMaxRowValues = 16384;
+template <int EPT>
+constexpr int max_lanes() { return (kMaxRowValues / EPT < 1024) ? kMaxRowValues / EPT : 1024; }
 constexpr float kLog2e = 1.4426950408889634f;
 
 // Lane `t` of a `nt`-lane workgroup owns vector slots t, t+nt, t+2nt, ... of
@@ -120,7 +127,7 @@ __device__ __forceinline__ float block_reduce(float x, float (*part)[kMaxWaves],
 }
 
 template <typename T, int EPT>
-__global__ __launch_bounds__(1024) void softmax_rows(const T* __restrict__ x, T* __restrict__ y,
+__global__ __launch_bounds__(max_lanes<EPT>()) void softmax_rows(const T* __restrict__ x, T* __restrict__ y,
                                                      int64_t xrs, int64_t yrs, int64_t rows,
                                                      int64_t cols, int rpp, int vec) {
   __shared__ float part[2][kMaxWaves];
@@ -153,7 +160,7 @@ __global__ __launch_bounds__(1024) void softmax_rows(const T* __restrict__ x, T*
 }
 
 template <typename T, int EPT>
-__global__ __launch_bounds__(1024) void rmsnorm_rows(const T* __restrict__ x,
+__global__ __launch_bounds__(max_lanes<EPT>()) void rmsnorm_rows(const T* __restrict__ x,
                                                      const T* __restrict__ gamma,
                                                      T* __restrict__ y, int64_t xrs, int64_t yrs,
                                                      int64_t rows, int64_t cols, float eps,
@@ -234,6 +241,11 @@ int check_row_config(int64_t rows, int64_t cols, int64_t xrs, int64_t yrs, int b
   if (xrs < cols || yrs < cols) {
     set_error("row strides (%lld, %lld) shorter than the row (%lld)", (long long)xrs,
               (long long)yrs, (long long)cols);
+    return KF_ERR_INVALID_ARGUMENT;
+  }
+  if (block_size > kMaxRowValues) {
+    set_error("row of %lld exceeds the single-pass limit of %d values per workgroup",
+              (long long)cols, kMaxRowValues);
     return KF_ERR_INVALID_ARGUMENT;
   }
   *ept = block_size >= waves * kWave ? block_size / (waves * kWave) : 1;

@@ -52,10 +52,19 @@ VECTOR_BYTES = 16
 #: property (the compiled 256x128x64 / 4-wave tile uses 228 VGPR + 136 AGPR).
 MAX_ACC_REGS_PER_LANE = 128
 
-#: Efficiency heuristic: total per-lane registers the tile model may claim
-#: (accumulators + fragments + staged global loads), leaving 64 of the 512
-#: for addresses, loop state and the epilogue.
-MAX_TILE_REGS_PER_LANE = 448
+#: Registers (VGPR + AGPR) a SIMD holds per lane. A workgroup of W waves puts
+#: ceil(W/4) waves on each SIMD, so each lane may use 512 / ceil(W/4).
+REGISTER_FILE_PER_LANE = 512
+
+#: Efficiency heuristic: of a lane's budget, this many are left for
+#: addresses, loop state and the epilogue; the tile model (accumulators +
+#: fragments + staged global loads) may claim the rest.
+RESERVED_REGS_PER_LANE = 64
+
+
+def register_budget(waves: int) -> int:
+    """Registers one lane may use when a workgroup of ``waves`` waves is resident."""
+    return REGISTER_FILE_PER_LANE // max(1, ceil_div(waves, 4))
 
 
 def next_power_of_2(n: int) -> int:
@@ -335,8 +344,12 @@ def gemm_instantiation_reason(
     regs = gemm_tile_regs(block_m, block_n, block_k, waves, elem, direct=direct)
     if regs["acc"] > MAX_ACC_REGS_PER_LANE:
         return f"register pressure: {regs['acc']} accumulator registers per lane"
-    if regs["total"] > MAX_TILE_REGS_PER_LANE:
-        return f"register file: {regs['total']} tile registers per lane"
+    budget = register_budget(waves) - RESERVED_REGS_PER_LANE
+    if regs["total"] > budget:
+        return (
+            f"register file: {regs['total']} tile registers per lane exceed the "
+            f"{budget} available at {waves} waves"
+        )
     return None
 
 
@@ -418,6 +431,8 @@ class _GemmSpace(SearchSpace):
     def _gemv_reason(self, config: KernelConfig, m: int, k: int, elem: int) -> str | None:
         warps, split = config["num_warps"], config["SPLIT_K"]
         mr = next_power_of_2(m)
+        if mr > 4 and warps > 8:
+            return f"register pressure: {mr} rows of x allow at most 8 waves, got {warps}"
         lds = warps * mr * 64 * (VECTOR_BYTES // elem) * 4
         if lds > self.GEMV_MAX_LDS:
             return f"LDS: wave reduction needs {lds // 1024} KiB at num_warps={warps}, M={m}"
@@ -516,17 +531,20 @@ class _RowReductionSpace(SearchSpace):
     NUM_WARPS = (1, 2, 4, 8, 16)
     ROWS_PER_PROGRAM = (1, 2, 4, 8)
 
-    #: fp32 values a lane holds for its share of the row. Hardware-derived:
-    #: 64 of the 256 VGPRs, leaving the rest for gamma (RMSNorm) and addresses.
+    #: fp32 values a lane holds for its share of the row: at most 64 (with
+    #: RMSNorm's gamma copy, 128 of a lane's registers).
     MIN_ELEMS_PER_LANE = 1
     MAX_ELEMS_PER_LANE = 64
 
-    #: Widest single-pass row: 64 values x 1024 lanes (16 waves, the
-    #: workgroup limit). The default configuration reaches exactly
-    #: MAX_ELEMS_PER_LANE at this width, mirroring the reference's tie
-    #: between its limit and its default (search.py:441-459).
+    #: Widest single-pass row: 16384 fp32 values (64 KiB) per workgroup in
+    #: registers. At 16 waves (1024 lanes, the workgroup limit) each lane may
+    #: use 128 registers, which holds 16 values plus gamma and addresses; the
+    #: kernels' launch bounds allow 16384/EPT lanes, so EPT=64 runs at <= 4
+    #: waves with 512 registers per lane. The default configuration uses 16
+    #: waves at this width. The value equals the reference's single-pass
+    #: limit (search.py:441-459), re-derived from the gfx950 register file.
     MAX_WAVES = 16
-    MAX_BLOCK_SIZE = MAX_ELEMS_PER_LANE * MAX_WAVES * 64
+    MAX_BLOCK_SIZE = 16384
 
     def grid(self, problem: Problem) -> Iterator[KernelConfig]:
         block = next_power_of_2(problem.dims_dict["cols"])

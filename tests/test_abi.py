@@ -1,0 +1,169 @@
+"""The C-ABI boundary, without a GPU.
+
+* libkernelo_amd.so loads and exports every function include/kernelo_amd.h
+  declares, and the ctypes binding (kernelo_amd.runtime.hip.SIGNATURES)
+  covers exactly that set.
+* Calls that never reach the HIP runtime behave as documented: version and
+  target queries, the variant table (which must equal the search space's
+  instantiation rules), workspace sizing, zero-size early returns and every
+  argument error, each with its KF_ERR_* code and a kf_last_error() message.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from kernelo_amd.runtime import hip
+from kernelo_amd.tuning.search import gemm_instantiations
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "kernelo_amd.h"
+
+
+def _declared() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^\s*(?:[\w\s\*]+?)\b(kf_\w+)\s*\(", text, flags=re.M))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return hip.load()
+
+
+def test_header_declares_the_expected_entry_points():
+    assert _declared() == {
+        "kf_abi_version", "kf_build_target", "kf_last_error",
+        "kf_gemm", "kf_gemm_has_variant", "kf_gemm_variant_count", "kf_gemm_variant_info",
+        "kf_gemv", "kf_gemv_workspace_bytes", "kf_softmax", "kf_rmsnorm",
+    }
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    declared = _declared()
+    assert declared == set(hip.SIGNATURES)
+    for name in declared:
+        assert getattr(lib, name) is not None  # AttributeError if not exported
+
+
+def test_identification(lib):
+    assert lib.kf_abi_version() == 1
+    assert lib.kf_build_target() == b"gfx950"
+
+
+def test_variant_table_equals_the_instantiation_rules(lib):
+    staged = gemm_instantiations()
+    direct = gemm_instantiations(direct=1)
+    expected = set()
+    for dt, elem in ((0, 4), (1, 2), (2, 2)):
+        expected |= {(dt, *t, hip.KF_PIPELINE_STAGED) for t in staged[elem]}
+        expected |= {(dt, *t, hip.KF_PIPELINE_DIRECT) for t in direct[elem]}
+    got = hip.gemm_variants()
+    assert len(got) == len(set(got)) == lib.kf_gemm_variant_count()
+    assert set(got) == expected
+    bm, bn, bk, w, s = staged[2][0]
+    assert lib.kf_gemm_has_variant(1, bm, bn, bk, w, s, 0) == 1
+    assert lib.kf_gemm_has_variant(1, 48, 48, 32, 4, 2, 0) == 0
+    assert lib.kf_gemm_has_variant(0, 256, 128, 64, 8, 2, 1) == 0  # no fp32 direct pipeline
+
+
+def test_workspace_sizing(lib):
+    assert lib.kf_gemv_workspace_bytes(1, 11008, 1) == 0
+    tickets = (-(-11008 // 64) * 4 + 255) // 256 * 256
+    assert lib.kf_gemv_workspace_bytes(1, 11008, 8) == tickets + 8 * 11008 * 4
+    assert lib.kf_gemv_workspace_bytes(0, 11008, 8) == 0
+
+
+def _rc_and_message(rc_fn):
+    rc = rc_fn()
+    return rc, hip.last_error()
+
+
+NULL = None
+
+
+def test_gemm_argument_errors(lib):
+    def gemm(dtype=1, m=64, n=64, k=64, epi=0, bm=64, bn=64, bk=64, w=4, st=2, gm=8, pipe=0,
+             a=1 << 20, b=1 << 20, c=1 << 20, bias=NULL):
+        return lib.kf_gemm(dtype, a, b, bias, c, m, n, k, k, 1, n, 1, n, 1, epi, bm, bn, bk, w, st,
+                           gm, pipe, NULL)
+
+    rc, msg = _rc_and_message(lambda: gemm(dtype=7))
+    assert rc == hip.KF_ERR_UNSUPPORTED_DTYPE and "dtype" in msg
+    rc, msg = _rc_and_message(lambda: gemm(m=-1))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "negative" in msg
+    rc, msg = _rc_and_message(lambda: gemm(epi=9))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "epilogue" in msg
+    rc, msg = _rc_and_message(lambda: gemm(gm=0))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "group_m" in msg
+    rc, msg = _rc_and_message(lambda: gemm(pipe=5))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "pipeline" in msg
+    rc, msg = _rc_and_message(lambda: gemm(bm=48))
+    assert rc == hip.KF_ERR_NOT_BUILT and "no compiled" in msg
+    rc, msg = _rc_and_message(lambda: gemm(epi=1))  # bias missing
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "bias" in msg
+    # Zero-size problems return before any launch.
+    assert gemm(m=0) == hip.KF_OK and gemm(n=0) == hip.KF_OK
+
+
+def test_gemv_argument_errors(lib):
+    def gemv(m=1, n=64, k=64, split=1, waves=4, ws=NULL, wsb=0, dtype=2, epi=0):
+        return lib.kf_gemv(dtype, 1 << 20, 1 << 20, NULL, 1 << 20, m, n, k, k, 1, n, 1, n, 1, epi,
+                           split, waves, ws, wsb, NULL)
+
+    rc, msg = _rc_and_message(lambda: gemv(m=9))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "decode limit" in msg
+    rc, msg = _rc_and_message(lambda: gemv(waves=17))
+    assert rc == hip.KF_ERR_OUT_OF_RESOURCES
+    rc, msg = _rc_and_message(lambda: gemv(split=0))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "split_k" in msg
+    rc, msg = _rc_and_message(lambda: gemv(split=4))
+    assert rc == hip.KF_ERR_WORKSPACE and "workspace" in msg
+    rc, msg = _rc_and_message(lambda: gemv(dtype=4))
+    assert rc == hip.KF_ERR_UNSUPPORTED_DTYPE
+    rc, msg = _rc_and_message(lambda: gemv(epi=1))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT
+    assert gemv(m=0) == hip.KF_OK
+
+
+def test_row_kernel_argument_errors(lib):
+    def softmax(cols=100, block=128, rpp=1, waves=1, rows=4, dtype=1):
+        return lib.kf_softmax(dtype, 1 << 20, 1 << 20, rows, cols, cols, cols, block, rpp, waves, NULL)
+
+    rc, msg = _rc_and_message(lambda: softmax(block=64))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "cannot hold a row" in msg
+    rc, msg = _rc_and_message(lambda: softmax(block=96))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "power of two" in msg
+    rc, msg = _rc_and_message(lambda: softmax(cols=20000, block=32768, waves=16))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "single-pass limit" in msg
+    rc, msg = _rc_and_message(lambda: softmax(waves=17))
+    assert rc == hip.KF_ERR_OUT_OF_RESOURCES
+    rc, msg = _rc_and_message(lambda: softmax(rpp=0))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT
+    rc, msg = _rc_and_message(lambda: softmax(block=256, waves=3))
+    assert rc == hip.KF_ERR_OUT_OF_RESOURCES and "per lane" in msg
+    rc, msg = _rc_and_message(lambda: softmax(dtype=9))
+    assert rc == hip.KF_ERR_UNSUPPORTED_DTYPE
+    assert softmax(rows=0) == hip.KF_OK
+    rc = lib.kf_rmsnorm(1, 1 << 20, 1 << 20, 1 << 20, 4, 100, 100, 100, ctypes.c_float(-1.0), 128,
+                        1, 1, NULL)
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "eps" in hip.last_error()
+
+
+def test_check_maps_codes_to_tuner_classified_exceptions():
+    with pytest.raises(hip.KernelNotCompiled):
+        hip.check(hip.KF_ERR_NOT_BUILT, "x")
+    with pytest.raises(hip.KernelOutOfResources):
+        hip.check(hip.KF_ERR_OUT_OF_RESOURCES, "x")
+    with pytest.raises(hip.KernelOutOfMemoryError):
+        hip.check(hip.KF_ERR_OUT_OF_MEMORY, "x")
+    with pytest.raises(hip.KernelWorkspaceError):
+        hip.check(hip.KF_ERR_WORKSPACE, "x")
+    hip.check(hip.KF_OK, "x")
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(hip.KernelLibraryNotCompiled, match="missing"):
+        hip.load(tmp_path / "nope.so")

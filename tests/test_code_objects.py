@@ -1,0 +1,120 @@
+"""Compile-time properties of our own gfx950 code objects (no GPU needed).
+
+The reference asserts on NVIDIA compiler output (tensor-core instructions, one
+exp per epilogue element, shared-memory sizes, no local memory). The same
+intent is checked here on the AMD code objects inside libkernelo_amd.so:
+kernel metadata from ``llvm-readelf --notes`` and instructions from
+``llvm-objdump -d`` of code this repository compiled.
+"""
+
+from __future__ import annotations
+
+import re
+
+import pytest
+
+from codeobj import load_kernels
+from kernelo_amd.runtime import hip
+from kernelo_amd.tuning.search import (
+    REGISTER_FILE_PER_LANE,
+    gemm_direct_lds_bytes,
+    gemm_instantiations,
+)
+
+
+@pytest.fixture(scope="module")
+def kernels():
+    hip.load()  # fails loudly if the library is not built
+    return load_kernels(str(hip.LIBRARY_PATH))
+
+
+def _gemm_params(name):
+    m = re.search(r"gemm_(direct_)?kernelI(f|DF16_|DF16b)((?:Li\d+E)+)", name)
+    if not m:
+        return None
+    ints = [int(x) for x in re.findall(r"Li(\d+)E", m.group(3))]
+    dtype = {"f": "fp32", "DF16_": "fp16", "DF16b": "bf16"}[m.group(2)]
+    return bool(m.group(1)), dtype, ints
+
+
+def test_every_kernel_is_present(kernels):
+    staged = gemm_instantiations()
+    direct = gemm_instantiations(direct=1)
+    n_gemm = 3 * (len(staged[4]) + 2 * len(staged[2])) + 2 * 2 * len(direct[2])
+    gemm = [n for n in kernels if _gemm_params(n)]
+    assert len(gemm) == n_gemm
+    assert sum("softmax_rows" in n for n in kernels) == 3 * 7
+    assert sum("rmsnorm_rows" in n for n in kernels) == 3 * 7
+    assert sum("gemv_splitk" in n for n in kernels) == 3 * 4
+
+
+def test_no_kernel_spills_to_scratch(kernels):
+    spilled = {n: k.private_bytes for n, k in kernels.items() if k.private_bytes}
+    assert not spilled
+
+
+def test_register_use_stays_in_the_file(kernels):
+    for name, k in kernels.items():
+        assert k.vgprs + k.agprs <= REGISTER_FILE_PER_LANE, name
+
+
+def test_mfma_instructions_match_the_dtype(kernels):
+    expect = {"fp16": "v_mfma_f32_16x16x32_f16", "bf16": "v_mfma_f32_16x16x32_bf16",
+              "fp32": "v_mfma_f32_16x16x4_f32"}
+    for name, k in kernels.items():
+        p = _gemm_params(name)
+        if p:
+            assert k.count(expect[p[1]]) > 0, name
+
+
+def test_direct_kernels_use_dma_and_transposing_reads(kernels):
+    seen = 0
+    for name, k in kernels.items():
+        p = _gemm_params(name)
+        if not p or not p[0]:
+            continue
+        seen += 1
+        direct, dtype, (bm, bn, waves, blayout) = p
+        assert k.count("global_load_lds_dwordx4") > 0, name
+        assert k.count("ds_read_b64_tr_b16") > 0 if blayout == 0 else True, name
+        # Static LDS = the search space's model of two dense stages, <= 160 KiB.
+        assert k.group_bytes == gemm_direct_lds_bytes(bm, bn, 2) <= 160 * 1024, name
+    assert seen > 0
+
+
+def test_staged_kernels_use_dynamic_lds_only(kernels):
+    for name, k in kernels.items():
+        p = _gemm_params(name)
+        if p and not p[0]:
+            assert k.group_bytes == 0, name  # sized at launch from the tile model
+
+
+def test_gelu_epilogue_is_one_exp_per_output_element(kernels):
+    for name, k in kernels.items():
+        p = _gemm_params(name)
+        if not p or p[0] or p[1] != "fp16":
+            continue
+        bm, bn, bk, waves, _, _ = p[2]
+        wm, wn = (2, 2) if waves == 4 else ((4, 2) if bm >= bn else (2, 4))
+        per_lane = (bm // wm) * (bn // wn) // 64
+        assert k.count("v_exp_f32") == per_lane, name
+
+
+def test_softmax_is_one_exp_per_element(kernels):
+    for name, k in kernels.items():
+        m = re.search(r"softmax_rowsI\w+?Li(\d+)E", name)
+        if m:
+            assert k.count("v_exp_f32") == int(m.group(1)), name
+
+
+def test_row_reductions_use_cross_lane_ops_and_one_barrier_per_reduction(kernels):
+    for name, k in kernels.items():
+        if "softmax_rows" in name:
+            assert k.count("s_barrier") == 2, name  # max, then sum
+        if "rmsnorm_rows" in name:
+            assert k.count("s_barrier") == 1, name
+        if "_rows" in name:
+            xlane = sum(k.count(op) for op in ("ds_bpermute_b32", "ds_swizzle_b32", "v_permlane32_swap_b32",
+                                               "v_permlane16_swap_b32")) + sum(
+                1 for line in k.asm if "row_" in line or "quad_perm" in line)
+            assert xlane >= 6, name

@@ -1,0 +1,245 @@
+"""Candidate generation: the generic pipeline and the gfx950 rules.
+
+The generic pipeline (enumerate -> named rejections -> conditional prune ->
+priority sort -> budget) is pinned against the reference's published counts
+by feeding it a restatement of the reference's CUDA-era rules
+(oracle/reference_search.py): 432/180/180/48 with rejections 105/81/30/27/9
+on A100 properties (README.md:67-81), 30 feasible for a 1x11008x4096 decode
+GEMM (README.md:91-94), 178 on RTX 4090 properties (README.md:95-96) and 48
+pruned at 512^3 (README.md:229-230). The gfx950 rules are then tested one
+by one, as the reference's tests/test_search.py does for its own.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from kernelo_amd.runtime.env import MI355X_CAPS
+from kernelo_amd.tuning.config import KernelConfig, Problem
+from kernelo_amd.tuning.search import (
+    DEFAULT_MAX_CANDIDATES,
+    MatmulSearchSpace,
+    RMSNormSearchSpace,
+    SoftmaxSearchSpace,
+    default_row_config,
+    gemm_instantiation_reason,
+    gemm_instantiations,
+    gemm_lds_bytes,
+    next_power_of_2,
+    search_space,
+)
+from oracle.reference_search import ReferenceGemmSpace, a100_caps, rtx4090_caps
+
+
+def _gemm(m=2048, n=4096, k=4096, dtype="fp16", op="matmul"):
+    return Problem.create(op, dtype, M=m, N=n, K=k)
+
+
+# --- the generic pipeline, pinned by the reference's published counts -------------
+
+
+def test_reference_rules_reproduce_published_counts():
+    result = ReferenceGemmSpace().generate(_gemm(), a100_caps())
+    assert (result.generated, result.feasible, result.after_prune, len(result.candidates)) == (
+        432, 180, 180, 48,
+    )
+    counts: dict[str, int] = {}
+    for _, reason in result.rejected:
+        key = reason.split(":")[0].split("(")[0].strip()
+        counts[key] = counts.get(key, 0) + 1
+    assert counts == {
+        "uncoalesced A tile": 105,
+        "tile too small": 81,
+        "uncoalesced B tile": 30,
+        "too little output per warp at num_warps=8": 27,
+        "register pressure": 9,
+    }
+
+
+def test_reference_rules_decode_and_device_counts():
+    decode = ReferenceGemmSpace().generate(_gemm(1, 11008, 4096), a100_caps())
+    assert decode.feasible == 30
+    assert all(c["BLOCK_M"] == 16 for c in decode.candidates)
+    assert ReferenceGemmSpace().generate(_gemm(), rtx4090_caps()).feasible == 178
+
+
+def test_reference_rules_prune_only_in_the_middle_regime():
+    mid = ReferenceGemmSpace().generate(_gemm(512, 512, 512), a100_caps())
+    assert mid.feasible - mid.after_prune == 48
+    assert all("underfilled" in r for _, r in mid.rejected[-48:])
+    tiny = ReferenceGemmSpace().generate(_gemm(64, 64, 64), a100_caps())
+    assert tiny.after_prune == tiny.feasible  # nothing fills the GPU: no prune
+
+
+def test_reference_explain_text_matches_published_breakdown():
+    text = ReferenceGemmSpace().explain(_gemm(), a100_caps())
+    for line in ("grid points      : 432", "feasible         : 180", "selected (budget): 48 of 48",
+                 "105  uncoalesced A tile", "81  tile too small"):
+        assert line in text
+
+
+# --- gfx950 GEMM rules ----------------------------------------------------------------
+
+
+def test_next_power_of_2():
+    assert [next_power_of_2(n) for n in (1, 2, 3, 4097, 11008)] == [1, 2, 4, 8192, 16384]
+    with pytest.raises(ValueError):
+        next_power_of_2(0)
+
+
+def test_mfma_k_step_rule_depends_on_dtype():
+    assert "MFMA k step" in gemm_instantiation_reason(128, 128, 16, 4, 2, 2, MI355X_CAPS)
+    assert gemm_instantiation_reason(128, 128, 16, 4, 2, 4, MI355X_CAPS) is None
+
+
+def test_lds_rule_uses_the_160_kib_limit():
+    # fp32 256x256x64 double-buffered with 16-byte row padding: 2*512*68*4 bytes.
+    assert gemm_lds_bytes(256, 256, 64, 2, 4) == 278528
+    reason = gemm_instantiation_reason(256, 256, 64, 8, 2, 4, MI355X_CAPS)
+    assert reason.startswith("LDS") and "160 KiB" in reason
+
+
+def test_register_rules_follow_the_per_lane_budget():
+    # 4 waves: one per SIMD, 512 registers per lane, but 256 accumulators are over the cap.
+    assert "register pressure" in gemm_instantiation_reason(256, 256, 64, 4, 2, 2, MI355X_CAPS)
+    # 8 waves: two per SIMD, 256 registers per lane. The register-staged pipeline
+    # needs 128 acc + 48 fragment + 32 staging registers and does not fit; the
+    # direct pipeline stages nothing in registers and does.
+    reason = gemm_instantiation_reason(256, 256, 64, 8, 2, 2, MI355X_CAPS)
+    assert reason.startswith("register file") and "8 waves" in reason
+    assert gemm_instantiation_reason(256, 256, 64, 8, 2, 2, MI355X_CAPS, direct=1) is None
+
+
+def test_wave_tile_rule():
+    assert "wave tile" in gemm_instantiation_reason(32, 32, 32, 8, 2, 2, MI355X_CAPS)
+
+
+def test_direct_rules():
+    assert gemm_instantiation_reason(256, 128, 64, 8, 2, 2, MI355X_CAPS, direct=1) is None
+    assert "16-bit" in gemm_instantiation_reason(128, 128, 32, 4, 2, 4, MI355X_CAPS, direct=1)
+    assert "BLOCK_K must be 64" in gemm_instantiation_reason(128, 128, 32, 4, 2, 2, MI355X_CAPS, direct=1)
+    assert "swizzle" in gemm_instantiation_reason(128, 32, 64, 4, 2, 2, MI355X_CAPS, direct=1)
+
+
+def test_flagship_gemm_space_on_mi355x():
+    result = MatmulSearchSpace().generate(_gemm(), MI355X_CAPS)
+    assert result.generated == 4 * 4 * 3 * 2 * 2
+    assert len(result.candidates) == DEFAULT_MAX_CANDIDATES
+    # Every rejection is attributed to a named rule.
+    assert all(":" in reason for _, reason in result.rejected)
+    # Large problem: every survivor fills the 256 CUs, so reuse decides and the
+    # first candidate is a 256-wide tile.
+    first = result.candidates[0]
+    assert first["BLOCK_M"] * first["BLOCK_N"] >= 128 * 256
+
+
+def test_candidates_are_deterministic():
+    a = MatmulSearchSpace().candidates(_gemm(), MI355X_CAPS)
+    b = MatmulSearchSpace().candidates(_gemm(), MI355X_CAPS)
+    assert a == b
+
+
+def test_budget_is_honoured():
+    assert len(MatmulSearchSpace().candidates(_gemm(), MI355X_CAPS, max_candidates=5)) == 5
+    with pytest.raises(ValueError):
+        MatmulSearchSpace(max_candidates=0)
+
+
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
+def test_decode_shapes_offer_split_k_gemv_first(m):
+    cands = MatmulSearchSpace().candidates(_gemm(m, 11008, 4096, "bf16"), MI355X_CAPS)
+    assert cands and cands[0].get("GEMV") == 1
+    assert any(c.get("GEMV") is None for c in cands)  # MFMA tiles stay in the running
+
+
+def test_gemv_rules():
+    space = MatmulSearchSpace()
+    problem = _gemm(1, 4096, 256, "bf16")
+    short = KernelConfig("matmul", GEMV=1, SPLIT_K=64, num_warps=16)
+    assert "split-K slice too short" in space.reject_reason(short, problem, MI355X_CAPS)
+    wide = KernelConfig("matmul", GEMV=1, SPLIT_K=1, num_warps=16)
+    assert "register pressure" in space.reject_reason(wide, _gemm(8, 4096, 4096, "bf16"), MI355X_CAPS)
+    big = KernelConfig("matmul", GEMV=1, SPLIT_K=1, num_warps=8)
+    assert "LDS" in space.reject_reason(big, _gemm(8, 4096, 4096, "bf16"), MI355X_CAPS)
+
+
+def test_no_gemv_candidates_above_eight_rows():
+    cands = MatmulSearchSpace().candidates(_gemm(9, 4096, 4096), MI355X_CAPS, max_candidates=1000)
+    assert not any(c.get("GEMV") for c in cands)
+
+
+def test_overshoot_rule_keeps_the_smallest_tile():
+    result = MatmulSearchSpace().generate(_gemm(1, 11008, 4096), MI355X_CAPS)
+    tiles = [c for c in result.candidates if not c.get("GEMV")]
+    assert tiles and all(c["BLOCK_M"] == 32 for c in tiles)
+
+
+def test_small_problems_prefer_parallelism():
+    cands = MatmulSearchSpace().candidates(_gemm(256, 256, 256), MI355X_CAPS)
+    first = cands[0]
+    assert first["BLOCK_M"] * first["BLOCK_N"] <= 64 * 64
+
+
+def test_space_rejects_mismatched_problem():
+    with pytest.raises(ValueError):
+        MatmulSearchSpace().generate(Problem.create("softmax", "fp16", rows=2, cols=2), MI355X_CAPS)
+    with pytest.raises(ValueError):
+        search_space("vector_add")
+
+
+def test_instantiation_list_is_the_rule_filtered_grid():
+    staged = gemm_instantiations(MI355X_CAPS)
+    direct = gemm_instantiations(MI355X_CAPS, direct=1)
+    assert len(staged[2]) == 59 and len(staged[4]) == 80 and len(direct[2]) == 20
+    assert direct[4] == [] and all(t[2] == 64 for t in direct[2])
+    for elem, tiles in staged.items():
+        for bm, bn, bk, w, s in tiles:
+            assert gemm_instantiation_reason(bm, bn, bk, w, s, elem, MI355X_CAPS) is None
+
+
+# --- row kernels -------------------------------------------------------------------------
+
+
+def test_row_space_shape():
+    problem = Problem.create("rmsnorm", "fp16", rows=4096, cols=4096)
+    result = RMSNormSearchSpace().generate(problem, MI355X_CAPS)
+    assert result.generated == 20
+    assert all(c["BLOCK_SIZE"] == 4096 for c in result.candidates)
+
+
+def test_row_space_rules():
+    space = SoftmaxSearchSpace()
+    p = Problem.create("softmax", "fp16", rows=4, cols=128)
+    reasons = {r.split(":")[0] for _, r in space.generate(p, MI355X_CAPS).rejected}
+    assert "idle lanes" in reasons
+    assert any("ROWS_PER_PROGRAM" in r for _, r in space.generate(p, MI355X_CAPS).rejected)
+    wide = Problem.create("softmax", "fp16", rows=4, cols=65537)
+    assert all("single-pass limit" in r for _, r in space.generate(wide, MI355X_CAPS).rejected)
+
+
+@pytest.mark.parametrize("cols", [1, 127, 4096, 11008, 16384])
+def test_default_row_config_is_feasible_up_to_the_limit(cols):
+    cfg = default_row_config("rmsnorm", cols)
+    problem = Problem.create("rmsnorm", "fp32", rows=8, cols=cols)
+    reason = RMSNormSearchSpace().reject_reason(cfg, problem, MI355X_CAPS)
+    if cols >= 64:
+        assert reason is None
+    per_lane = cfg["BLOCK_SIZE"] / (cfg["num_warps"] * 64)
+    assert per_lane <= RMSNormSearchSpace.MAX_ELEMS_PER_LANE
+    if cols == RMSNormSearchSpace.MAX_BLOCK_SIZE:
+        # At the limit the default fills the workgroup: 16 waves x 16 values.
+        assert cfg["num_warps"] == 16 and per_lane == 16
+
+
+def test_single_pass_limit_is_sixteen_thousand_values():
+    assert RMSNormSearchSpace.MAX_BLOCK_SIZE == 16384
+    p = Problem.create("rmsnorm", "fp32", rows=8, cols=16385)
+    assert all("single-pass limit" in r for _, r in RMSNormSearchSpace().generate(p, MI355X_CAPS).rejected)
+
+
+def test_explain_names_the_device_and_every_stage():
+    text = MatmulSearchSpace().explain(_gemm(), MI355X_CAPS)
+    assert "MI355X" in text and "256 CUs" in text and "160 KiB LDS" in text
+    for stage in ("grid points", "feasible", "after prune", "selected (budget)"):
+        assert stage in text
