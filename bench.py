@@ -53,12 +53,31 @@ def _time_steps(fn, steps: int, warmup: int, flush) -> list[float]:
     return [start[i].elapsed_time(end[i]) for i in range(steps)]
 
 
-def _cpu_time(fn, iters: int) -> float:
+def _cpu_time(fn, seconds: float) -> tuple[float, int]:
+    """Mean seconds per call over at least ``seconds`` of calls (after one warm call)."""
     fn()  # warm caches / thread pool
     t0 = time.perf_counter()
-    for _ in range(iters):
+    iters = 0
+    while True:
         fn()
-    return (time.perf_counter() - t0) / iters
+        iters += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            return elapsed / iters, iters
+
+
+def _traffic(name: str) -> float | None:
+    """HBM bytes per launch for ``name`` from the committed rocprofv3 counter summary.
+
+    ``profiles/hbm_traffic.json`` holds FETCH_SIZE + WRITE_SIZE per dispatch of each
+    configuration's kernel, scaled by what the same counters read for a copy of
+    known size; absent entries leave ``traffic`` null.
+    """
+    path = REPO / "profiles" / "hbm_traffic.json"
+    if not path.exists():
+        return None
+    entry = json.loads(path.read_text()).get("kernels", {}).get(name)
+    return None if entry is None else float(entry["traffic_bytes"])
 
 
 def main(argv: list[str] | None = None) -> int:
@@ -127,7 +146,7 @@ def main(argv: list[str] | None = None) -> int:
                 "peak": peak,
                 "unit": "TFLOP/s" if unit == "TFLOP/s" else "GB/s",
                 "frac": rate / peak,
-                "traffic": None,
+                "traffic": _traffic(name),
             },
         }
         if extra:
@@ -209,49 +228,44 @@ def main(argv: list[str] | None = None) -> int:
            metrics.matmul_bytes(1, 11008, 4096, 2), "GB/s", hbm, src)
 
     # --- CPU baseline: the oracle on the host cores, bounded slices ----------------
+    # About 4 s of calls per workload (about 20 s in all), on bounded slices of the
+    # same inputs; the headline is the GEMM slice.
     cpu = None
     if not args.no_cpu_baseline:
         from oracle import ops
 
         cores = host_cores()
         torch.set_num_threads(cores)
+        budget = 4.0
+
+        def cpu_entry(fn, work, unit, sample):
+            secs, iters = _cpu_time(fn, budget)
+            scale = 1e12 if unit == "TFLOP/s" else 1e9
+            return {"value": work / secs / scale, "unit": unit, "cores": cores, "kind": "port",
+                    "sample": f"{sample}; mean of {iters} calls over {secs * iters:.1f} s"}
+
         rows = 256
         ca, cb = a[:rows].cpu(), b.cpu()
-        secs = _cpu_time(lambda: ops.matmul_ref(ca, cb), 3)
-        cpu = {
-            "value": metrics.matmul_flops(rows, N, K) / secs / 1e12,
-            "unit": "TFLOP/s",
-            "cores": cores,
-            "kind": "port",
-            "sample": f"oracle matmul_ref (torch fp32 on CPU) on A[:{rows}] @ B, "
-                      f"{rows}x{N}x{K}, mean of 3 after 1 warmup",
-        }
+        cpu = cpu_entry(lambda: ops.matmul_ref(ca, cb), metrics.matmul_flops(rows, N, K), "TFLOP/s",
+                        f"oracle matmul_ref (torch fp32 on CPU) on A[:{rows}] @ B, {rows}x{N}x{K}")
         results["gemm_fp16_2048x4096x4096"]["cpu_baseline"] = cpu
-        secs = _cpu_time(lambda: ops.rmsnorm_ref(x, gamma, 1e-6), 5)
-        results["rmsnorm_fp32_4096x4096"]["cpu_baseline"] = {
-            "value": metrics.rmsnorm_bytes(4096, 4096, 4) / secs / 1e9, "unit": "GB/s",
-            "cores": cores, "kind": "port", "sample": "oracle rmsnorm_ref, full [4096,4096]",
-        }
+        results["rmsnorm_fp32_4096x4096"]["cpu_baseline"] = cpu_entry(
+            lambda: ops.rmsnorm_ref(x, gamma, 1e-6), metrics.rmsnorm_bytes(4096, 4096, 4), "GB/s",
+            "oracle rmsnorm_ref, full [4096,4096] fp32")
         cs = (3.0 * torch.randn(1024, 4096, generator=g)).to(torch.float16)
-        secs = _cpu_time(lambda: ops.softmax_ref(cs), 5)
-        results["softmax_fp16_8192x4096"]["cpu_baseline"] = {
-            "value": metrics.softmax_bytes(1024, 4096, 2) / secs / 1e9, "unit": "GB/s",
-            "cores": cores, "kind": "port", "sample": "oracle softmax_ref on [1024,4096] fp16",
-        }
+        results["softmax_fp16_8192x4096"]["cpu_baseline"] = cpu_entry(
+            lambda: ops.softmax_ref(cs), metrics.softmax_bytes(1024, 4096, 2), "GB/s",
+            "oracle softmax_ref on [1024,4096] fp16")
         cvx, cvw = vx.cpu(), vw.cpu()
-        secs = _cpu_time(lambda: ops.matmul_ref(cvx, cvw), 3)
-        results["gemv_bf16_1x11008x4096"]["cpu_baseline"] = {
-            "value": metrics.matmul_bytes(1, 11008, 4096, 2) / secs / 1e9, "unit": "GB/s",
-            "cores": cores, "kind": "port", "sample": "oracle matmul_ref, full 1x11008x4096 bf16",
-        }
-        fxs, fws, fbs = (torch.randn(64, FK, generator=g) / 64).to(torch.float16), \
-            (torch.randn(FK, FN, generator=g) / 64).to(torch.float16), fb.cpu()
-        secs = _cpu_time(lambda: ops.linear_gelu_ref(fxs, fws, fbs), 2)
-        results["fused_linear_fp16_4096x11008x4096"]["cpu_baseline"] = {
-            "value": metrics.matmul_flops(64, FN, FK) / secs / 1e12, "unit": "TFLOP/s",
-            "cores": cores, "kind": "port",
-            "sample": f"oracle linear_gelu_ref on X[:64], 64x{FN}x{FK}",
-        }
+        results["gemv_bf16_1x11008x4096"]["cpu_baseline"] = cpu_entry(
+            lambda: ops.matmul_ref(cvx, cvw), metrics.matmul_bytes(1, 11008, 4096, 2), "GB/s",
+            "oracle matmul_ref, full 1x11008x4096 bf16")
+        fxs = (torch.randn(64, FK, generator=g) / 64).to(torch.float16)
+        fws = (torch.randn(FK, FN, generator=g) / 64).to(torch.float16)
+        fbs = fb.cpu()
+        results["fused_linear_fp16_4096x11008x4096"]["cpu_baseline"] = cpu_entry(
+            lambda: ops.linear_gelu_ref(fxs, fws, fbs), metrics.matmul_flops(64, FN, FK), "TFLOP/s",
+            f"oracle linear_gelu_ref on X[:64], 64x{FN}x{FK}")
 
     line = {
         "metric": METRIC,

@@ -155,7 +155,7 @@ _TILES = [
     (128, 128, 64, 4, 0),
     (256, 128, 64, 4, 0),
     (128, 256, 32, 8, 0),
-    (256, 256, 64, 8, 0),
+    (256, 256, 32, 8, 0),
     (64, 256, 64, 8, 0),
     (64, 64, 64, 4, 1),
     (128, 128, 64, 4, 1),
@@ -215,6 +215,17 @@ def test_fused_linear_correctness(m, n, k, dtype):
     bias = _randn(n, dtype=dtype, seed=7)
     out = fused_linear_gelu(x.to(DEV), w.to(DEV), bias.to(DEV))
     _gate(ops.linear_gelu_ref(x, w, bias), out, dtype, f"fused {m}x{n}x{k}")
+
+
+def test_staged_tile_that_was_not_built_is_reported():
+    from kernelo_amd.kernels.matmul import matmul
+    from kernelo_amd.runtime import hip
+
+    a = torch.ones(64, 64, dtype=torch.float16, device=DEV)
+    cfg = KernelConfig("matmul", BLOCK_M=256, BLOCK_N=256, BLOCK_K=64, GROUP_M=8, DIRECT=0,
+                       num_warps=8, num_stages=2)
+    with pytest.raises(hip.KernelNotCompiled):
+        matmul(a, a, config=cfg)
 
 
 def test_fused_linear_transposed_weight():
