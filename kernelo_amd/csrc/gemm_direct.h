@@ -2,25 +2,41 @@
 //
 // Differences from the register-staged kernel in gemm_impl.h:
 //   * Global -> LDS with global_load_lds_dwordx4: each lane's 16 bytes land at
-//     (wave base + 16*lane) in LDS without passing through VGPRs, so the
-//     staging registers and the ds_write instructions disappear and the
-//     accumulators get the register file.
+//     (M0 + 16*lane) in LDS without passing through VGPRs. The loads use the
+//     scalar-base form: one wave-uniform SGPR base per operand and k-slice and
+//     one 32-bit per-lane byte offset per chunk that is fixed for the whole
+//     K loop, so the DMA costs almost no VGPRs.
+//   * STAGES (2 or 3) LDS buffers; with 3, slices t+1 and t+2 are in flight
+//     while slice t is multiplied. Each wave waits (vmcnt) for exactly its own
+//     loads of the next slice, then a plain s_barrier publishes them: the
+//     fences of __syncthreads() would wait for every outstanding load,
+//     including the prefetch of slice t+2.
+//   * The DMA is issued from inline assembly so the compiler's wait-count
+//     pass does not track it; every wait for it is explicit. (Untracked
+//     in-order loads can only make the compiler's own waits longer.)
 //   * No padding: LDS rows are dense and 16-byte chunks are XOR-swizzled by
-//     row, which is what keeps both the DMA writes (a wave fills 1 KiB of
-//     consecutive LDS) and the fragment reads bank-conflict free.
+//     row. The swizzles keep the fragment reads conflict-free for 16 or 32
+//     lanes per LDS cycle and leave the per-lane offsets invariant under the
+//     row steps the code adds as immediates.
 //   * Row-major B stays n-contiguous in LDS and is read with
 //     ds_read_b64_tr_b16: within a 16-lane group, lane i addressing
 //     (row0 + i/4, col0 + 4*(i%4)) receives column col0+i of rows
 //     row0..row0+3, which is the MFMA B-operand layout. Two such reads give
 //     the 8 consecutive k a v_mfma_f32_16x16x32 lane needs.
+//   * The second 32-wide k step of each slice is multiplied after the
+//     barrier, while the next slice's first fragments are read, so every
+//     wave has MFMAs to issue during its own LDS latency.
 //
 // Requirements (checked on the host): 16-bit dtype, A k-contiguous with a
 // 16-byte aligned base and row pitch, B either n-contiguous (BLAYOUT 0) or
 // k-contiguous (BLAYOUT 1) with the same alignment, N (BLAYOUT 0) and K
-// multiples of 8. BK is 64: one A row of a k-slice is exactly 128 bytes.
-// M/N edges clamp rows/columns (results discarded); a partial last k-slice
-// has its chunks past K zeroed in LDS after the DMA lands.
+// multiples of 8, and per-lane byte offsets (BM rows of A, 64 k-rows or BN
+// rows of B) below 4 GiB. BK is 64: one A row of a k-slice is 128 bytes.
+// M/N edges clamp rows/columns (results discarded); the partial last k-slice
+// clamps k into range and zeroes its chunks past K after the DMA lands.
 #pragma once
+
+#include <type_traits>
 
 #include "gemm_impl.h"
 
@@ -48,17 +64,56 @@ __device__ __forceinline__ uint64_t ds_read_tr4<bf16>(const char* p) {
   return __builtin_bit_cast(uint64_t, v);
 }
 
-// DMA 16 bytes per lane into LDS at lds_wave_base + 16*lane.
-__device__ __forceinline__ void dma16(const void* gptr, char* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(gptr, (KF_LDS void*)(lds_wave_base), 16, 0, 0);
+__device__ __forceinline__ uint32_t lds_offset(const char* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((KF_LDS const char*)(p)));
 }
 
-__device__ __forceinline__ void wait_dma() {
-  // s_waitcnt vmcnt(0), leaving expcnt/lgkmcnt unconstrained (gfx9 encoding).
-  __builtin_amdgcn_s_waitcnt(0x0F70);
+// A wave-uniform pointer, moved into SGPRs for the scalar-base load form.
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const void*>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-template <int BM, int BN, int WAVES, int BLAYOUT>
+// 16 bytes per lane from (sbase + voff) into LDS at lds + 16*lane; sbase and
+// lds are wave-uniform. M0 holds the LDS address for the instruction.
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(uniform_ptr(sbase)), "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) with expcnt and lgkmcnt unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier for the DMA pipeline: this wave's LDS reads and writes
+// are complete (lgkmcnt(0)); its DMA was waited for explicitly before.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt/expcnt unconstrained
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Swizzled 16-byte chunk of a k-contiguous row (8 chunks per 128-byte row)
+// and of an n-contiguous B row of ROW_CHUNKS chunks. Both depend on row bits
+// below 16 only; rows r and r + 4 of n-contiguous B share the swizzle.
+__device__ __forceinline__ int swz_k(int chunk, int row) {
+  return chunk ^ ((row & 7) ^ ((row >> 3) & 1));
+}
+template <int ROW_CHUNKS>
+__device__ __forceinline__ int swz_n(int chunk, int row) {
+  if constexpr (ROW_CHUNKS >= 16) return chunk ^ (((row & 3) | ((row >> 1) & 4)) << 1);
+  return chunk ^ ((row & 3) << 1);
+}
+
+template <int BM, int BN, int WAVES, int STAGES>
 struct DirectTile {
   static constexpr int BK = kDirectBK;
   static constexpr int NT = WAVES * kWave;
@@ -72,38 +127,32 @@ struct DirectTile {
   static constexpr int kABytes = BM * BK * 2;
   static constexpr int kBBytes = BN * BK * 2;
   static constexpr int kStageBytes = kABytes + kBBytes;
-  static constexpr int kLdsBytes = 2 * kStageBytes;  // static LDS (two stage objects)
+  static constexpr int kLdsBytes = STAGES * kStageBytes;  // static LDS
   // 16-byte chunks per stage and DMA instructions per lane.
-  static constexpr int kAChunks = BM * BK / 8;
-  static constexpr int kBChunks = BN * BK / 8;
-  static constexpr int kAIters = kAChunks / NT;
-  static constexpr int kBIters = kBChunks / NT;
-  // B row (BLAYOUT 0: one k-row of BN elements) in chunks.
-  static constexpr int kBRowChunks = BN / 8;
-  static_assert(kAChunks % NT == 0 && kBChunks % NT == 0, "DMA must tile the stage exactly");
+  static constexpr int kAIters = BM * BK / 8 / NT;
+  static constexpr int kBIters = BN * BK / 8 / NT;
+  static constexpr int kPer = kAIters + kBIters;  // vector-memory instructions per slice
+  static constexpr int kBRowChunks = BN / 8;      // BLAYOUT 0: chunks per k-row of B
+  static_assert(STAGES == 2 || STAGES == 3, "two or three LDS stages");
+  static_assert((BM * BK / 8) % NT == 0 && (BN * BK / 8) % NT == 0, "DMA must tile the stage");
   static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile must be whole 16x16 fragments");
-  static_assert(BLAYOUT == 1 || BN >= 64, "n-contiguous B swizzle needs >= 8 chunks per row");
+  static_assert(2 * kPer < 64, "outstanding DMA must fit the vmcnt counter");
 };
 
-// Swizzled chunk position within a row.
-__device__ __forceinline__ int swz_k(int chunk, int row) { return chunk ^ (row & 7); }   // k-contig rows
-__device__ __forceinline__ int swz_n(int chunk, int row) { return chunk ^ ((row & 3) << 1); }  // n-contig rows
-
-template <typename T, int BM, int BN, int WAVES, int BLAYOUT>
+template <typename T, int BM, int BN, int WAVES, int BLAYOUT, int STAGES>
 __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
-  using Tl = DirectTile<BM, BN, WAVES, BLAYOUT>;
+  using Tl = DirectTile<BM, BN, WAVES, STAGES>;
   constexpr int BK = Tl::BK;
   constexpr int NT = Tl::NT;
   constexpr int FM = Tl::FM, FN = Tl::FN;
+  constexpr int kPer = Tl::kPer;
+  static_assert(BLAYOUT == 1 || BN >= 64, "n-contiguous B needs >= 8 chunks per k-row");
 
-  // One LDS object per stage: with distinct objects the compiler can prove
-  // that the DMA into one stage does not alias fragment reads of the other,
-  // so it does not wait for the DMA before the reads.
-  __shared__ __attribute__((aligned(16))) char stage0[Tl::kStageBytes];
-  __shared__ __attribute__((aligned(16))) char stage1[Tl::kStageBytes];
+  __shared__ __attribute__((aligned(16))) char lds[Tl::kLdsBytes];
+  char* const s0 = lds;
+  char* const s1 = lds + Tl::kStageBytes;
+  char* const s2 = lds + (STAGES == 3 ? 2 * Tl::kStageBytes : 0);
 
-  const T* __restrict__ A = static_cast<const T*>(args.A);
-  const T* __restrict__ B = static_cast<const T*>(args.B);
   const int64_t M = args.M, N = args.N, K = args.K;
 
   // ---- tile order: regroup per XCD, then GROUP_M bands (as gemm_kernel) ----
@@ -122,92 +171,111 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / Tl::WN;
   const int wn = wave % Tl::WN;
 
-  // ---- DMA sources ------------------------------------------------------------
-  // Each lane owns fixed chunks of a stage: a row pointer plus the chunk's k
-  // offset within the slice (A and k-contiguous B), or a column pointer plus
-  // the slice-relative k row (n-contiguous B). Chunk q = j*NT + tid is
-  // written to LDS slot q; its logical chunk is the slot position XOR the
-  // row's swizzle.
-  const T* a_row[Tl::kAIters];
-  int a_k[Tl::kAIters];
+  // ---- DMA sources: tile bases + per-lane byte offsets -----------------------
+  // Chunk q = j*NT + tid is written to LDS slot q; its source is the chunk at
+  // the slot's position XOR the row's swizzle. Rows past M (and columns or
+  // rows of B past N) are clamped to the last valid one.
+  const char* const a_tile = static_cast<const char*>(args.A) + m0 * args.lda_m * 2;
+  const int64_t lda_b = args.lda_m * 2;
+  const int64_t ldb_b = (BLAYOUT == 0 ? args.ldb_k : args.ldb_n) * 2;  // bytes per B row
+  const char* const b_tile = static_cast<const char*>(args.B) + (BLAYOUT == 0 ? n0 * 2 : n0 * ldb_b);
+  constexpr int kRowsPerIter = NT / 8;  // k-contiguous rows (A, BLAYOUT 1) per DMA instruction
+  const int kr = tid >> 3;              // this lane's row within an instruction's rows
+  const int kc = swz_k(tid & 7, kr) * 8;  // its k within the slice; same for every j
+  uint32_t a_off[Tl::kAIters];
 #pragma unroll
   for (int j = 0; j < Tl::kAIters; ++j) {
-    const int q = j * NT + tid;
-    const int r = q >> 3;
-    int64_t row = m0 + r;
-    row = row < M ? row : M - 1;
-    a_row[j] = A + row * args.lda_m;
-    a_k[j] = swz_k(q & 7, r) * 8;
+    int64_t r = j * kRowsPerIter + kr;
+    r = (m0 + r < M) ? r : (M - 1 - m0);
+    a_off[j] = static_cast<uint32_t>(r * lda_b + kc * 2);
   }
-  const T* b_ptr[Tl::kBIters];
-  int b_k[Tl::kBIters];
+  uint32_t b_off[Tl::kBIters];
+  int b_row[Tl::kBIters];  // BLAYOUT 0: k-row of the chunk within the slice
 #pragma unroll
   for (int j = 0; j < Tl::kBIters; ++j) {
     const int q = j * NT + tid;
     if constexpr (BLAYOUT == 0) {
-      const int r = q / Tl::kBRowChunks;  // k row within the slice
-      int64_t col = n0 + swz_n(q % Tl::kBRowChunks, r) * 8;
-      col = col < N ? col : N - 8;
-      b_ptr[j] = B + col;
-      b_k[j] = r;
+      const int r = q / Tl::kBRowChunks;
+      int64_t col = swz_n<Tl::kBRowChunks>(q % Tl::kBRowChunks, r) * 8;
+      col = (n0 + col < N) ? col : (N - 8 - n0);
+      b_row[j] = r;
+      b_off[j] = static_cast<uint32_t>(r * ldb_b + col * 2);
     } else {
-      const int r = q >> 3;  // n row
-      int64_t row = n0 + r;
-      row = row < N ? row : N - 1;
-      b_ptr[j] = B + row * args.ldb_n;
-      b_k[j] = swz_k(q & 7, r) * 8;
+      int64_t r = j * kRowsPerIter + kr;
+      r = (n0 + r < N) ? r : (N - 1 - n0);
+      b_row[j] = 0;
+      b_off[j] = static_cast<uint32_t>(r * ldb_b + kc * 2);
     }
   }
+  const uint32_t lds_lane0 = static_cast<uint32_t>(wave * 64 * 16);
 
-  // Enqueue the DMA of k-slice kt into the stage at `base`. Sources past K
-  // (only in a partial last slice) are clamped to the last valid k so every
-  // address stays inside the operand; zero_tail() later overwrites them.
-  auto issue = [&](char* base, int64_t kt) {
+  const int64_t nk = ceil_div(K, BK);
+  const bool ktail = (K % BK) != 0;
+
+  // Enqueue the DMA of k-slice kt into `stage`.
+  auto issue_full = [&](const char* stage, int64_t kt) {
+    const uint32_t la = lds_offset(stage) + lds_lane0;
+    const char* ab = a_tile + kt * BK * 2;
+    const char* bb = b_tile + (BLAYOUT == 0 ? kt * BK * ldb_b : kt * BK * 2);
+#pragma unroll
+    for (int j = 0; j < Tl::kAIters; ++j) dma16(ab, a_off[j], la + j * NT * 16);
+#pragma unroll
+    for (int j = 0; j < Tl::kBIters; ++j) dma16(bb, b_off[j], la + Tl::kABytes + j * NT * 16);
+  };
+  // The partial last slice: k is clamped into range per lane so every source
+  // stays inside its operand (K % 8 == 0, so K - 8 >= k0); the chunks past K
+  // are zeroed by zero_tail() once the DMA has landed.
+  auto issue_last = [&](const char* stage, int64_t kt) {
+    const uint32_t la = lds_offset(stage) + lds_lane0;
     const int64_t k0 = kt * BK;
+    int64_t k = k0 + kc;
+    k = k < K ? k : K - 8;
+    const uint32_t dk = static_cast<uint32_t>((k - k0) * 2) - static_cast<uint32_t>(kc * 2);
+    const char* ab = a_tile + k0 * 2;
 #pragma unroll
-    for (int j = 0; j < Tl::kAIters; ++j) {
-      int64_t k = k0 + a_k[j];
-      k = k < K ? k : K - 8;
-      dma16(a_row[j] + k, base + (j * NT + wave * 64) * 16);
-    }
+    for (int j = 0; j < Tl::kAIters; ++j) dma16(ab, a_off[j] + dk, la + j * NT * 16);
+    if constexpr (BLAYOUT == 0) {
+      const char* bb = b_tile + k0 * ldb_b;
 #pragma unroll
-    for (int j = 0; j < Tl::kBIters; ++j) {
-      int64_t k = k0 + b_k[j];
-      if constexpr (BLAYOUT == 0) {
-        k = k < K ? k : K - 1;
-        dma16(b_ptr[j] + k * args.ldb_k, base + Tl::kABytes + (j * NT + wave * 64) * 16);
-      } else {
-        k = k < K ? k : K - 8;
-        dma16(b_ptr[j] + k, base + Tl::kABytes + (j * NT + wave * 64) * 16);
+      for (int j = 0; j < Tl::kBIters; ++j) {
+        int64_t kb = k0 + b_row[j];
+        kb = kb < K ? kb : K - 1;
+        const uint32_t off = b_off[j] - static_cast<uint32_t>(b_row[j] * ldb_b) +
+                             static_cast<uint32_t>((kb - k0) * ldb_b);
+        dma16(bb, off, la + Tl::kABytes + j * NT * 16);
       }
+    } else {
+      const char* bb = b_tile + k0 * 2;
+#pragma unroll
+      for (int j = 0; j < Tl::kBIters; ++j) dma16(bb, b_off[j] + dk, la + Tl::kABytes + j * NT * 16);
     }
   };
-
-  // Zero the chunks of a partial k-slice that lie past K (after its DMA landed).
-  auto zero_tail = [&](char* base, int64_t k0) {
+  auto issue = [&](const char* stage, int64_t kt) {
+    if (ktail && kt == nk - 1)
+      issue_last(stage, kt);
+    else
+      issue_full(stage, kt);
+  };
+  // Zero the chunks of slice kt that lie past K (after its DMA landed).
+  auto fix = [&](char* stage, int64_t kt) {
+    if (!(ktail && kt == nk - 1)) return;
+    const int64_t k0 = kt * BK;
     const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int j = 0; j < Tl::kAIters; ++j) {
-      const int q = j * NT + tid;
-      const int c = swz_k(q & 7, q >> 3);
-      if (k0 + c * 8 >= K) *reinterpret_cast<u32x4*>(base + q * 16) = z;
-    }
+    for (int j = 0; j < Tl::kAIters; ++j)
+      if (k0 + kc >= K) *reinterpret_cast<u32x4*>(stage + (j * NT + tid) * 16) = z;
 #pragma unroll
     for (int j = 0; j < Tl::kBIters; ++j) {
-      const int q = j * NT + tid;
-      int kk;
-      if constexpr (BLAYOUT == 0)
-        kk = q / Tl::kBRowChunks;
-      else
-        kk = swz_k(q & 7, q >> 3) * 8;
-      if (k0 + kk >= K) *reinterpret_cast<u32x4*>(base + Tl::kABytes + q * 16) = z;
+      const int64_t kk = BLAYOUT == 0 ? k0 + b_row[j] : k0 + kc;
+      if (kk >= K) *reinterpret_cast<u32x4*>(stage + Tl::kABytes + (j * NT + tid) * 16) = z;
     }
   };
 
+  // ---- fragments ----------------------------------------------------------------
   f32x4 acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
@@ -216,69 +284,141 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
 
   const int g = lane >> 4;   // lane group: k offset 8*g within a 32-wide step
   const int li = lane & 15;  // row (A) / column (B) within a fragment
-
-  auto compute = [&](const char* As) {
-    const char* Bs = As + Tl::kABytes;
+  // Stage-relative byte offsets of this lane's fragments for k step c. Rows
+  // i*16 apart share the swizzle, so fragment i adds i*16 rows as an immediate.
+  const int ar = wm * Tl::TM + li;
+  int a_frag[2];
+  int b_frag[2][FN];
 #pragma unroll
-    for (int kc = 0; kc < BK / 32; ++kc) {
-      u32x4 af[FM], bfr[FN];
+  for (int c = 0; c < 2; ++c) {
+    a_frag[c] = ar * 128 + swz_k(c * 4 + g, ar) * 16;
 #pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int r = wm * Tl::TM + i * 16 + li;
-        af[i] = *reinterpret_cast<const u32x4*>(As + r * 128 + swz_k(kc * 4 + g, r) * 16);
+    for (int j = 0; j < FN; ++j) {
+      if constexpr (BLAYOUT == 0) {
+        const int col = wn * Tl::TN + j * 16 + (li & 3) * 4;
+        const int r0 = c * 32 + 8 * g + (li >> 2);  // rows r0 and r0 + 4 share the swizzle
+        b_frag[c][j] = Tl::kABytes + r0 * (BN * 2) + swz_n<Tl::kBRowChunks>(col >> 3, r0) * 16 + (col & 7) * 2;
+      } else {
+        const int br = wn * Tl::TN + j * 16 + li;
+        b_frag[c][j] = Tl::kABytes + br * 128 + swz_k(c * 4 + g, br) * 16;
       }
+    }
+  }
+  auto load_frags = [&](const char* S, int c, u32x4 (&af)[FM], u32x4 (&bf)[FN]) {
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        if constexpr (BLAYOUT == 0) {
-          // Two transposing reads: k rows kc*32 + 8g + {0..3, 4..7} of column li.
-          const int col = wn * Tl::TN + j * 16 + (li & 3) * 4;
-          uint64_t lo, hi;
-          {
-            const int r = kc * 32 + 8 * g + (li >> 2);
-            const int c = col >> 3;
-            lo = ds_read_tr4<T>(Bs + r * (BN * 2) + swz_n(c, r) * 16 + (col & 7) * 2);
-          }
-          {
-            const int r = kc * 32 + 8 * g + 4 + (li >> 2);
-            const int c = col >> 3;
-            hi = ds_read_tr4<T>(Bs + r * (BN * 2) + swz_n(c, r) * 16 + (col & 7) * 2);
-          }
-          bfr[j] = u32x4{static_cast<uint32_t>(lo), static_cast<uint32_t>(lo >> 32),
-                         static_cast<uint32_t>(hi), static_cast<uint32_t>(hi >> 32)};
-        } else {
-          const int r = wn * Tl::TN + j * 16 + li;
-          bfr[j] = *reinterpret_cast<const u32x4*>(Bs + r * 128 + swz_k(kc * 4 + g, r) * 16);
-        }
+    for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const u32x4*>(S + a_frag[c] + i * 16 * 128);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      if constexpr (BLAYOUT == 0) {
+        const uint64_t lo = ds_read_tr4<T>(S + b_frag[c][j]);
+        const uint64_t hi = ds_read_tr4<T>(S + b_frag[c][j] + 4 * BN * 2);
+        bf[j] = u32x4{static_cast<uint32_t>(lo), static_cast<uint32_t>(lo >> 32),
+                      static_cast<uint32_t>(hi), static_cast<uint32_t>(hi >> 32)};
+      } else {
+        bf[j] = *reinterpret_cast<const u32x4*>(S + b_frag[c][j]);
       }
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) Mma<T>::run(af[i], bfr[j], acc[i][j]);
     }
   };
-
-  // ---- main loop: DMA of slice t+1 overlaps the MFMAs of slice t -----------
-  // Unrolled by two so that each half names its stage objects at compile time.
-  const int64_t nk = ceil_div(K, BK);
-  auto step = [&](char* cur, char* nxt, int64_t kt) {
-    const bool more = kt + 1 < nk;
-    if (more) issue(nxt, kt + 1);
-    compute(cur);
-    if (more) {
-      wait_dma();
-      if ((kt + 2) * BK > K) zero_tail(nxt, (kt + 1) * BK);
-    }
-    __syncthreads();
+  auto mma_all = [&](const u32x4 (&af)[FM], const u32x4 (&bf)[FN]) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) Mma<T>::run(af[i], bf[j], acc[i][j]);
   };
+  // Step 1 of each slice is carried over and multiplied after the barrier,
+  // while step 0 of the next slice loads (sched_barrier keeps the reads first).
+  u32x4 ca[FM], cb[FN];
+  using First = std::integral_constant<bool, true>;
+  using Next = std::integral_constant<bool, false>;
+  auto compute = [&](const char* S, auto first) {
+    u32x4 af[FM], bf[FN];
+    load_frags(S, 0, af, bf);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!decltype(first)::value) mma_all(ca, cb);
+    load_frags(S, 1, ca, cb);
+    mma_all(af, bf);
+  };
+
+  // ---- main loop ------------------------------------------------------------------
+  // Steps whose prefetch is known to exist run unconditionally with their
+  // stages named at compile time; the first and last steps are generic.
   if (nk > 0) {
-    issue(stage0, 0);
-    wait_dma();
-    if (BK > K) zero_tail(stage0, 0);
-    __syncthreads();
-    for (int64_t kt = 0; kt < nk; kt += 2) {
-      step(stage0, stage1, kt);
-      if (kt + 1 < nk) step(stage1, stage0, kt + 1);
+    if constexpr (STAGES == 2) {
+      issue(s0, 0);
+      wait_vm<0>();
+      fix(s0, 0);
+      lds_barrier();
+      auto step = [&](char* cur, char* nxt, int64_t t, auto first) {
+        if (t < nk) {
+          if (t + 1 < nk) issue(nxt, t + 1);
+          compute(cur, first);
+          wait_vm<0>();
+          if (t + 1 < nk) fix(nxt, t + 1);
+          lds_barrier();
+        }
+      };
+      step(s0, s1, 0, First{});
+      int64_t kt = 1;
+      for (; kt + 3 <= nk; kt += 2) {  // slices kt (s1) and kt+1 (s0)
+        issue(s0, kt + 1);             // kt+1 <= nk-2: never the partial slice
+        compute(s1, Next{});
+        wait_vm<0>();
+        lds_barrier();
+        issue(s1, kt + 2);             // kt+2 may be the partial last slice
+        compute(s0, Next{});
+        wait_vm<0>();
+        fix(s1, kt + 2);
+        lds_barrier();
+      }
+      step(s1, s0, kt, Next{});
+      step(s0, s1, kt + 1, Next{});
+    } else {
+      issue(s0, 0);
+      if (nk > 1) {
+        issue(s1, 1);
+        wait_vm<kPer>();
+      } else {
+        wait_vm<0>();
+      }
+      fix(s0, 0);
+      lds_barrier();
+      auto step = [&](char* cur, char* nxt, char* pre, int64_t t, auto first) {
+        if (t < nk) {
+          if (t + 2 < nk) issue(pre, t + 2);
+          compute(cur, first);
+          if (t + 2 < nk)
+            wait_vm<kPer>();
+          else
+            wait_vm<0>();
+          if (t + 1 < nk) fix(nxt, t + 1);
+          lds_barrier();
+        }
+      };
+      step(s0, s1, s2, 0, First{});
+      int64_t kt = 1;
+      // Slices kt (s1), kt+1 (s2), kt+2 (s0). The slices waited for here
+      // (kt+1..kt+3 <= nk-2) are never the partial one; kt+4 may be, and the
+      // step that waits for it (t = kt+3, below or in the next trip) zeroes it.
+      for (; kt + 5 <= nk; kt += 3) {
+        issue(s0, kt + 2);
+        compute(s1, Next{});
+        wait_vm<kPer>();
+        lds_barrier();
+        issue(s1, kt + 3);
+        compute(s2, Next{});
+        wait_vm<kPer>();
+        lds_barrier();
+        issue(s2, kt + 4);
+        compute(s0, Next{});
+        wait_vm<kPer>();
+        lds_barrier();
+      }
+      step(s1, s2, s0, kt, Next{});
+      step(s2, s0, s1, kt + 1, Next{});
+      step(s0, s1, s2, kt + 2, Next{});
+      step(s1, s2, s0, kt + 3, Next{});
     }
+    mma_all(ca, cb);  // step 1 of the last slice
   }
 
   // ---- epilogue -------------------------------------------------------------

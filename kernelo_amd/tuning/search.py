@@ -270,12 +270,14 @@ def gemm_tile_regs(
 ) -> dict[str, int]:
     """Per-lane register model of one tile: accumulators, fragments, staged loads.
 
-    The direct pipeline stages nothing in registers (the DMA writes LDS).
+    The direct pipeline stages nothing in registers (the DMA writes LDS) but
+    holds two k steps of fragments: one carried across the barrier while the
+    next slice's first step loads.
     """
     lanes = waves * 64
     wm, wn = wave_grid(waves, block_m, block_n)
     acc = block_m * block_n // lanes
-    frags = 4 * (block_m // wm // MFMA_TILE + block_n // wn // MFMA_TILE)
+    frags = 4 * (block_m // wm // MFMA_TILE + block_n // wn // MFMA_TILE) * (2 if direct else 1)
     staged = 0 if direct else 4 * ceil_div((block_m + block_n) * block_k * elem, VECTOR_BYTES * lanes)
     return {"acc": acc, "frags": frags, "staged": staged, "total": acc + frags + staged}
 
@@ -326,6 +328,8 @@ def gemm_instantiation_reason(
         reason = gemm_direct_reason(block_m, block_n, block_k, waves, stages, elem, caps)
         if reason is not None:
             return reason
+    elif stages != 2:
+        return f"pipeline: the register-staged pipeline is double-buffered, not {stages}-stage"
     kstep = MFMA_K[elem]
     if block_k % kstep:
         return f"MFMA k step: BLOCK_K={block_k} is not a multiple of {kstep} for {elem}-byte inputs"
@@ -360,7 +364,9 @@ class _GemmSpace(SearchSpace):
     BLOCK_N = (32, 64, 128, 256)
     BLOCK_K = (16, 32, 64)
     NUM_WARPS = (4, 8)
-    NUM_STAGES = (2,)
+    #: LDS stages: the register-staged pipeline is double-buffered; the DMA
+    #: pipeline can keep two slices in flight with a third stage.
+    NUM_STAGES = (2, 3)
     #: 0: register-staged LDS pipeline; 1: global->LDS DMA pipeline.
     DIRECT = (0, 1)
     GROUP_M = 8
@@ -452,7 +458,9 @@ class _GemmSpace(SearchSpace):
         GEMM tiles: (1) workgroups, saturating at one per CU, so that a large
         problem ties and a small one prefers filling the GPU; (2) reuse
         ``BM*BN/(BM+BN)`` -- the MFMA work per byte staged through LDS;
-        (3) least padding waste; then fewer waves (more registers each).
+        (3) least padding waste; then the DMA pipeline, more stages in
+        flight, and its 8-wave form (two waves per SIMD hide LDS latency);
+        register-staged tiles prefer fewer waves (more registers each).
         GEMV: HBM-bound, so (1) at least one workgroup per CU, (2) at least
         eight waves per CU (each keeps 8 x 1 KiB row segments in flight, and
         HBM needs ~32 KiB in flight per CU), then fewer slices (less partial-sum
@@ -480,7 +488,10 @@ class _GemmSpace(SearchSpace):
             -reuse,
             waste,
             -config.get("DIRECT", 0),
-            config["num_warps"],
+            -config["num_stages"],
+            # The DMA pipeline hides LDS latency with two waves per SIMD; the
+            # register-staged one prefers fewer, larger-register waves.
+            -config["num_warps"] if config.get("DIRECT") else config["num_warps"],
         )
 
 

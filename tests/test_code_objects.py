@@ -74,11 +74,11 @@ def test_direct_kernels_use_dma_and_transposing_reads(kernels):
         if not p or not p[0]:
             continue
         seen += 1
-        direct, dtype, (bm, bn, waves, blayout) = p
+        direct, dtype, (bm, bn, waves, blayout, stages) = p
         assert k.count("global_load_lds_dwordx4") > 0, name
         assert k.count("ds_read_b64_tr_b16") > 0 if blayout == 0 else True, name
-        # Static LDS = the search space's model of two dense stages, <= 160 KiB.
-        assert k.group_bytes == gemm_direct_lds_bytes(bm, bn, 2) <= 160 * 1024, name
+        # Static LDS = the search space's model of the dense stages, <= 160 KiB.
+        assert k.group_bytes == gemm_direct_lds_bytes(bm, bn, stages) <= 160 * 1024, name
     assert seen > 0
 
 

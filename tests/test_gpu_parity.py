@@ -149,27 +149,33 @@ def test_matmul_correctness_suite(m, n, k, dtype):
     _gate(ops.matmul_ref(a, b), out, dtype, f"matmul {m}x{n}x{k}")
 
 
+# (BLOCK_M, BLOCK_N, BLOCK_K, waves, DIRECT, stages)
 _TILES = [
-    (32, 32, 32, 4, 0),
-    (64, 64, 64, 4, 0),
-    (128, 128, 64, 4, 0),
-    (256, 128, 64, 4, 0),
-    (128, 256, 32, 8, 0),
-    (256, 256, 32, 8, 0),
-    (64, 256, 64, 8, 0),
-    (64, 64, 64, 4, 1),
-    (128, 128, 64, 4, 1),
-    (128, 128, 64, 8, 1),
-    (256, 128, 64, 8, 1),
-    (256, 256, 64, 8, 1),
-    (128, 256, 64, 4, 1),
+    (32, 32, 32, 4, 0, 2),
+    (64, 64, 64, 4, 0, 2),
+    (128, 128, 64, 4, 0, 2),
+    (256, 128, 64, 4, 0, 2),
+    (128, 256, 32, 8, 0, 2),
+    (256, 256, 32, 8, 0, 2),
+    (64, 256, 64, 8, 0, 2),
+    (32, 64, 64, 4, 1, 2),
+    (64, 64, 64, 4, 1, 3),
+    (128, 128, 64, 4, 1, 2),
+    (128, 128, 64, 8, 1, 3),
+    (256, 128, 64, 8, 1, 2),
+    (256, 128, 64, 8, 1, 3),
+    (128, 256, 64, 8, 1, 3),
+    (128, 256, 64, 4, 1, 3),
+    (256, 64, 64, 8, 1, 3),
 ]
 
 
 @pytest.mark.parametrize("tile", _TILES, ids=lambda t: "x".join(map(str, t)))
 @pytest.mark.parametrize("layout", ("nn", "nt", "tn"))
 @pytest.mark.parametrize(
-    "m,n,k", [(257, 513, 129), (1023, 4097, 127), (512, 512, 512), (300, 520, 136), (64, 64, 8)]
+    "m,n,k",
+    [(257, 513, 129), (1023, 4097, 127), (512, 512, 512), (300, 520, 136), (64, 64, 8),
+     (300, 520, 200), (200, 264, 456)],
 )
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16), ids=("fp16", "bf16"))
 def test_matmul_tiles_and_layouts(tile, layout, m, n, k, dtype):
@@ -178,7 +184,7 @@ def test_matmul_tiles_and_layouts(tile, layout, m, n, k, dtype):
     are not multiples of 8 (the DMA path zeroes chunks past K)."""
     from kernelo_amd.kernels.matmul import matmul
 
-    bm, bn, bk, w, direct = tile
+    bm, bn, bk, w, direct, stages = tile
     a = _randn(m, k, dtype=dtype, seed=1)
     b = _randn(k, n, dtype=dtype, seed=2)
     da, db = a.to(DEV), b.to(DEV)
@@ -188,7 +194,7 @@ def test_matmul_tiles_and_layouts(tile, layout, m, n, k, dtype):
         da = a.t().contiguous().to(DEV).t()
     cfg = KernelConfig(
         "matmul", BLOCK_M=bm, BLOCK_N=bn, BLOCK_K=bk, GROUP_M=8, DIRECT=direct, num_warps=w,
-        num_stages=2,
+        num_stages=stages,
     )
     out = matmul(da, db, config=cfg)
     _gate(ops.matmul_ref(a, b), out, dtype, f"{cfg} {layout} {m}x{n}x{k}")
@@ -337,8 +343,8 @@ def _guarded_call(m, n, k, cfg, seed, dtype=torch.bfloat16):
     else:
         rc = lib.kf_gemm(abi_code(dtype), da.data_ptr(), db.data_ptr(), None, cptr, m, n, k,
                          da.stride(0), da.stride(1), db.stride(0), db.stride(1), pitch, 1, 0,
-                         cfg["BLOCK_M"], cfg["BLOCK_N"], cfg["BLOCK_K"], cfg["num_warps"], 2, 8,
-                         int(cfg.get("DIRECT", 0)), stream)
+                         cfg["BLOCK_M"], cfg["BLOCK_N"], cfg["BLOCK_K"], cfg["num_warps"],
+                         cfg.get("num_stages", 2), 8, int(cfg.get("DIRECT", 0)), stream)
     hip.check(rc, "guarded call")
     torch.cuda.synchronize()
     host = buf.cpu().view(m + 2 * pad, pitch).float()
@@ -355,7 +361,9 @@ def _guarded_call(m, n, k, cfg, seed, dtype=torch.bfloat16):
         (1023, 4097, 127, KernelConfig("matmul", BLOCK_M=256, BLOCK_N=128, BLOCK_K=64, GROUP_M=8, num_warps=4, num_stages=2)),
         (1023, 4097, 127, KernelConfig("matmul", BLOCK_M=32, BLOCK_N=64, BLOCK_K=32, GROUP_M=8, num_warps=4, num_stages=2)),
         (1023, 4096, 136, KernelConfig("matmul", BLOCK_M=128, BLOCK_N=128, BLOCK_K=64, GROUP_M=8, DIRECT=1, num_warps=4, num_stages=2)),
-        (1000, 1032, 72, KernelConfig("matmul", BLOCK_M=256, BLOCK_N=256, BLOCK_K=64, GROUP_M=8, DIRECT=1, num_warps=8, num_stages=2)),
+        (1000, 1032, 72, KernelConfig("matmul", BLOCK_M=256, BLOCK_N=128, BLOCK_K=64, GROUP_M=8, DIRECT=1, num_warps=8, num_stages=3)),
+        (1000, 1032, 1000, KernelConfig("matmul", BLOCK_M=128, BLOCK_N=256, BLOCK_K=64, GROUP_M=8, DIRECT=1, num_warps=8, num_stages=3)),
+        (777, 1032, 328, KernelConfig("matmul", BLOCK_M=256, BLOCK_N=128, BLOCK_K=64, GROUP_M=8, DIRECT=1, num_warps=8, num_stages=2)),
         (1, 7, 3, KernelConfig("matmul", GEMV=1, SPLIT_K=1, num_warps=1)),
         (1, 7, 3, KernelConfig("matmul", GEMV=1, SPLIT_K=2, num_warps=4)),
         (1, 7, 3, KernelConfig("matmul", BLOCK_M=32, BLOCK_N=32, BLOCK_K=32, GROUP_M=8, num_warps=4, num_stages=2)),

@@ -103,16 +103,28 @@ def test_lds_rule_uses_the_160_kib_limit():
 def test_register_rules_follow_the_per_lane_budget():
     # 4 waves: one per SIMD, 512 registers per lane, but 256 accumulators are over the cap.
     assert "register pressure" in gemm_instantiation_reason(256, 256, 64, 4, 2, 2, MI355X_CAPS)
-    # 8 waves: two per SIMD, 256 registers per lane. The register-staged pipeline
-    # needs 128 acc + 48 fragment + 32 staging registers and does not fit; the
-    # direct pipeline stages nothing in registers and does.
+    # 8 waves: two per SIMD, 256 registers per lane less a 64-register reserve.
+    # The register-staged pipeline needs 128 acc + 48 fragment + 32 staging
+    # registers and does not fit; the direct pipeline stages nothing in
+    # registers but carries a second k step of fragments (128 + 2*48), which
+    # does not fit either. At 256x128 it does: 64 acc + 2*32 fragments.
     reason = gemm_instantiation_reason(256, 256, 64, 8, 2, 2, MI355X_CAPS)
     assert reason.startswith("register file") and "8 waves" in reason
-    assert gemm_instantiation_reason(256, 256, 64, 8, 2, 2, MI355X_CAPS, direct=1) is None
+    reason = gemm_instantiation_reason(256, 256, 64, 8, 2, 2, MI355X_CAPS, direct=1)
+    assert reason.startswith("register file")
+    assert gemm_instantiation_reason(256, 128, 64, 8, 3, 2, MI355X_CAPS, direct=1) is None
 
 
 def test_wave_tile_rule():
     assert "wave tile" in gemm_instantiation_reason(32, 32, 32, 8, 2, 2, MI355X_CAPS)
+
+
+def test_stage_rules():
+    # Three stages only for the DMA pipeline, and only where they fit in LDS.
+    assert "double-buffered" in gemm_instantiation_reason(128, 128, 64, 4, 3, 2, MI355X_CAPS)
+    assert gemm_instantiation_reason(256, 128, 64, 8, 3, 2, MI355X_CAPS, direct=1) is None
+    reason = gemm_instantiation_reason(256, 256, 64, 8, 3, 2, MI355X_CAPS, direct=1)
+    assert reason.startswith("LDS") and "192 KiB" in reason
 
 
 def test_direct_rules():
@@ -124,7 +136,7 @@ def test_direct_rules():
 
 def test_flagship_gemm_space_on_mi355x():
     result = MatmulSearchSpace().generate(_gemm(), MI355X_CAPS)
-    assert result.generated == 4 * 4 * 3 * 2 * 2
+    assert result.generated == 4 * 4 * 3 * 2 * 2 * 2  # BM x BN x BK x waves x stages x pipeline
     assert len(result.candidates) == DEFAULT_MAX_CANDIDATES
     # Every rejection is attributed to a named rule.
     assert all(":" in reason for _, reason in result.rejected)
@@ -191,7 +203,7 @@ def test_space_rejects_mismatched_problem():
 def test_instantiation_list_is_the_rule_filtered_grid():
     staged = gemm_instantiations(MI355X_CAPS)
     direct = gemm_instantiations(MI355X_CAPS, direct=1)
-    assert len(staged[2]) == 59 and len(staged[4]) == 80 and len(direct[2]) == 20
+    assert len(staged[2]) == 59 and len(staged[4]) == 80 and len(direct[2]) == 38
     assert direct[4] == [] and all(t[2] == 64 for t in direct[2])
     for elem, tiles in staged.items():
         for bm, bn, bk, w, s in tiles:
