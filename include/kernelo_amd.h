@@ -114,17 +114,20 @@ int kf_gemm_variant_info(int index, int* dtype, int* block_m, int* block_n, int*
  * Split-K GEMV for decode shapes: y[M,N] = x[M,K] @ W[K,N], M <= 8.
  * The reference runs decode through the same matmul at M=1
  * (kernels/matmul.py:132-155, tuning/search.py:377-386); this is its
- * HBM-bound replacement. Partial sums over `split_k` slices of K are reduced
- * deterministically (fixed order) by the last workgroup of each column
- * block, using a caller-provided workspace of kf_gemv_workspace_bytes()
- * bytes whose counter region must be zero before the first call (the
- * kernel leaves it zero again). epilogue as for kf_gemm.
+ * HBM-bound replacement. A workgroup of `waves` wavefronts owns a strip of
+ * lanes_per_row (8, 16, 32 or 64) 16-byte vectors of columns and one of
+ * `split_k` slices of K. Partial sums over the slices are reduced
+ * deterministically (fixed order) by the last workgroup of each strip, using
+ * a caller-provided workspace of kf_gemv_workspace_bytes() bytes whose
+ * counter region must be zero before the first call (the kernel leaves it
+ * zero again). epilogue as for kf_gemm.
  */
 int kf_gemv(int dtype, const void* x, const void* W, const void* bias, void* y,
             int64_t M, int64_t N, int64_t K,
             int64_t ldx_m, int64_t ldx_k, int64_t ldw_k, int64_t ldw_n,
             int64_t ldy_m, int64_t ldy_n, int epilogue,
-            int split_k, int waves, void* workspace, size_t workspace_bytes, void* stream);
+            int split_k, int waves, int lanes_per_row, void* workspace, size_t workspace_bytes,
+            void* stream);
 size_t kf_gemv_workspace_bytes(int64_t M, int64_t N, int split_k);
 
 /*

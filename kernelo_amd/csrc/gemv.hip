@@ -1,16 +1,23 @@
 // Split-K GEMV for decode-shaped products, y[M,N] = x[M,K] @ W[K,N], M <= 8.
 //
-// HBM-bound: every byte of W is read exactly once. A workgroup owns a strip of
-// 64*V columns (one 16-byte vector per lane, V = 16/sizeof(T)) and one of
-// `split_k` slices of K; its waves stride through the slice's rows so each
-// wave issues fully coalesced 1 KiB row segments. Waves are combined through
-// LDS, slices through an fp32 workspace: the last workgroup to finish a
-// column strip (atomic ticket) sums the slices in fixed order, so results
-// are bitwise reproducible run to run.
+// HBM-bound: every byte of W is read exactly once. A workgroup owns a strip
+// of LPR*V columns (LPR lanes of 16-byte vectors, V = 16/sizeof(T)) and one
+// of `split_k` slices of K. A wave load covers 64/LPR rows of the strip, so
+// the workgroup's waves hold nwaves*64/LPR row groups that stride through the
+// slice with U rows in flight per lane. Narrow strips give many workgroups
+// (hundreds for a decode-sized W) with few slices, so the cross-slice tail
+// stays short while every CU streams.
+//
+// Reduction, all in fixed order so results are bitwise reproducible run to
+// run: the row groups of a wave by lane shuffles, the waves through LDS, the
+// slices through an fp32 workspace -- the last workgroup to finish a strip
+// (atomic ticket) sums the slices in ascending order.
 //
 // The reference has no GEMV: decode runs through matmul_kernel with
 // BLOCK_M=16 (kernels/matmul.py:54-113, tuning/search.py:377-386).
 #include <math.h>
+
+#include <type_traits>
 
 #include "common.h"
 
@@ -19,8 +26,8 @@ namespace kf {
 namespace {
 
 constexpr int kGemvMaxWaves = 16;
-constexpr int kGemvUnroll = 8;        // rows of W in flight per lane
 constexpr size_t kGemvMaxLds = 64 * 1024;  // dynamic LDS without an opt-in attribute
+constexpr int kMinStripColumns = 32;       // LPR=8 lanes x 4 fp32 columns
 constexpr float kGeluC = 1.5957691216057308f;  // 2*sqrt(2/pi)
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -30,31 +37,42 @@ __device__ __forceinline__ float gelu_tanh(float a) {
   return a / (1.0f + __builtin_amdgcn_exp2f(-inner * kLog2e));
 }
 
-// Eight x rows need 8x the accumulators and x values: cap the workgroup at
-// 512 lanes so each lane may use 256 registers.
+// Registers per lane: one x row keeps 16 rows of W (64 registers) in
+// flight, two keep 8, more keep 4, and all of a trip's loads are live at
+// once; eight x rows need 8x the accumulators and x values. Only four rows
+// fit 128 registers (a 1024-lane workgroup); the others cap it at 512 lanes
+// (256 registers each).
 template <int MR>
-constexpr int gemv_max_lanes() { return MR > 4 ? 512 : 1024; }
+constexpr int gemv_max_lanes() { return MR == 4 ? 1024 : 512; }
+template <int MR>
+constexpr int gemv_unroll() { return MR <= 1 ? 16 : (MR <= 2 ? 8 : 4); }
 
-template <typename T, int MR>
+template <typename T, int MR, int LPR>
 __global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_splitk(
     const T* __restrict__ x, const T* __restrict__ W, const T* __restrict__ bias,
     T* __restrict__ y, int64_t M, int64_t N, int64_t K, int64_t ldx_m, int64_t ldx_k,
     int64_t ldw_k, int64_t ldw_n, int64_t ldy_m, int64_t ldy_n, int epilogue, int split_k,
     int vec, float* __restrict__ ws, unsigned* __restrict__ tickets) {
   constexpr int V = Vec<T>::N;
-  constexpr int BN = kWave * V;
+  constexpr int RPW = kWave / LPR;  // rows per wave load
+  constexpr int BN = LPR * V;       // columns per strip
+  constexpr int U = gemv_unroll<MR>();
   // red[wave][m][column]: nwaves*MR*BN floats of dynamic LDS.
   extern __shared__ float red[];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int nwaves = blockDim.x / kWave;
+  const int nthreads = blockDim.x;
+  const int sub = lane / LPR;                 // row of the wave load
+  const int cv = (lane % LPR) * V;            // column of the lane's vector within the strip
   const int64_t nb = blockIdx.x;
-  const int64_t col0 = nb * BN + static_cast<int64_t>(lane) * V;
+  const int64_t col0 = nb * BN + cv;
   const int s = blockIdx.y;
   const int64_t kc = ceil_div(K, split_k);
   const int64_t kbeg = static_cast<int64_t>(s) * kc;
   const int64_t kend = (kbeg + kc < K) ? kbeg + kc : K;
+  const int64_t step = static_cast<int64_t>(nwaves) * RPW;  // row groups
   // With aligned rows and N a multiple of V every lane's vector is either
   // wholly inside [0, N) or wholly past it. Lanes past N load a clamped,
   // valid vector whose sums are never stored, so one branch-free loop serves
@@ -81,28 +99,34 @@ __global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_splitk(
       for (int e = 0; e < V; ++e) acc[m][e] = __builtin_fmaf(xv[m], to_f32(w[e]), acc[m][e]);
   };
 
-  int64_t k = kbeg + wave;
-  const int64_t step = nwaves;
+  int64_t k = kbeg + wave * RPW + sub;
   if (vec_path) {
     const T* wcol = W + col_ld;
-    // kGemvUnroll rows per wave per trip. The x values go first so that the
-    // wait for them does not also wait for the W rows behind them; then all
-    // W loads issue back to back and are consumed in order.
-    for (; k + (kGemvUnroll - 1) * step < kend; k += kGemvUnroll * step) {
-      float xv[kGemvUnroll][MR];
+    // U rows per lane per trip. The x values go first so that the wait for
+    // them does not also wait for the W rows behind them; then all W loads
+    // issue back to back and are consumed in order.
+    for (; k + (U - 1) * step < kend; k += U * step) {
+      T xt[U][MR];
 #pragma unroll
-      for (int u = 0; u < kGemvUnroll; ++u)
+      for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int m = 0; m < MR; ++m) xv[u][m] = to_f32(xrow[m][(k + u * step) * ldx_k]);
-      u32x4 raw[kGemvUnroll];
+        for (int m = 0; m < MR; ++m) xt[u][m] = xrow[m][(k + u * step) * ldx_k];
+      u32x4 raw[U];
 #pragma unroll
-      for (int u = 0; u < kGemvUnroll; ++u)
+      for (int u = 0; u < U; ++u)
         raw[u] = *reinterpret_cast<const u32x4*>(wcol + (k + u * step) * ldw_k);
+      // Every load of the trip is issued before any value is used: without
+      // this the scheduler converts each x right after its load and waits
+      // for it, serialising the trip's memory latencies.
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int u = 0; u < kGemvUnroll; ++u) {
+      for (int u = 0; u < U; ++u) {
+        float xv[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) xv[m] = to_f32(xt[u][m]);
         T w[V];
         __builtin_memcpy(w, &raw[u], 16);
-        fma_row(xv[u], w);
+        fma_row(xv, w);
       }
     }
     for (; k < kend; k += step) {
@@ -127,135 +151,150 @@ __global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_splitk(
     }
   }
 
-  // Combine waves in fixed order through LDS.
+  // Rows of one wave load: lanes LPR apart hold the same columns. Butterfly
+  // over those lane bits, so every lane ends with the wave's sum.
 #pragma unroll
-  for (int m = 0; m < MR; ++m)
+  for (int off = LPR; off < kWave; off <<= 1)
 #pragma unroll
-    for (int e = 0; e < V; ++e) red[(wave * MR + m) * BN + lane * V + e] = acc[m][e];
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+      for (int e = 0; e < V; ++e) acc[m][e] += __shfl_xor(acc[m][e], off, kWave);
+  if (sub == 0) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+      for (int e = 0; e < V; ++e) red[(wave * MR + m) * BN + cv + e] = acc[m][e];
+  }
   __syncthreads();
-  if (wave != 0) return;
-#pragma unroll
-  for (int m = 0; m < MR; ++m)
-#pragma unroll
-    for (int e = 0; e < V; ++e) {
-      float r = red[m * BN + lane * V + e];
-      for (int w = 1; w < nwaves; ++w) r += red[(w * MR + m) * BN + lane * V + e];
-      acc[m][e] = r;
-    }
 
+  // From here each thread owns columns t, t + nthreads, ... of the strip and
+  // combines the waves in ascending order.
+  const int t = threadIdx.x;
+  auto wave_sum = [&](int m, int c) {
+    float r = 0.f;
+    for (int w = 0; w < nwaves; ++w) r += red[(w * MR + m) * BN + c];
+    return r;
+  };
   if (split_k > 1) {
     // Publish this slice's partial sums, then take a ticket for the strip.
     // The partials move through agent-scope relaxed atomic stores/loads,
     // which are coherent across XCDs without writing back or invalidating
     // whole L2s (what a device-scope fence costs here); the only ordering
-    // needed is that the stores have completed before the ticket is taken.
+    // needed is that every thread's stores have completed before the
+    // workgroup's ticket is taken.
+    for (int c = t; c < BN; c += nthreads) {
+      const int64_t col = nb * BN + c;
+      if (col >= N) continue;
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      if (m >= M) break;
-      float* dst = ws + (static_cast<int64_t>(s) * M + m) * N;
-#pragma unroll
-      for (int e = 0; e < V; ++e)
-        if (col0 + e < N)
-          __hip_atomic_store(dst + col0 + e, acc[m][e], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+      for (int m = 0; m < MR; ++m) {
+        if (m >= M) break;
+        __hip_atomic_store(ws + (static_cast<int64_t>(s) * M + m) * N + col, wave_sum(m, c),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the partial stores are done
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial stores are done
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    unsigned ticket = 0;
-    if (lane == 0)
+    __shared__ unsigned ticket;
+    __syncthreads();  // every thread's stores are done
+    if (t == 0)
       ticket = __hip_atomic_fetch_add(&tickets[nb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    ticket = __shfl(ticket, 0, kWave);
+    __syncthreads();
     if (ticket != static_cast<unsigned>(split_k - 1)) return;
     // Sum the slices in ascending order (deterministic). kSliceBatch slices'
     // loads are issued before any is added, so they are in flight together.
     constexpr int kSliceBatch = 4;
-    const int64_t cl = (col0 < N) ? col0 : N - 1;  // lanes past N read a valid column
+    for (int c = t; c < BN; c += nthreads) {
+      const int64_t col = nb * BN + c;
+      const int64_t cl = (col < N) ? col : N - 1;  // threads past N read a valid column
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        if (m >= M) break;
+        const float* src = ws + static_cast<int64_t>(m) * N + cl;
+        float r = 0.f;
+        for (int q0 = 0; q0 < split_k; q0 += kSliceBatch) {
+          float part[kSliceBatch];
+#pragma unroll
+          for (int b = 0; b < kSliceBatch; ++b) {
+            const int q = (q0 + b < split_k) ? q0 + b : split_k - 1;
+            part[b] = __hip_atomic_load(src + static_cast<int64_t>(q) * M * N, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+          }
+#pragma unroll
+          for (int b = 0; b < kSliceBatch; ++b)
+            if (q0 + b < split_k) r += part[b];
+        }
+        if (col >= N) continue;
+        if (epilogue == KF_EPILOGUE_BIAS_GELU) r = gelu_tanh(r + to_f32(bias[col]));
+        y[m * ldy_m + col * ldy_n] = from_f32<T>(r);
+      }
+    }
+    if (t == 0) __hip_atomic_store(&tickets[nb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+
+  for (int c = t; c < BN; c += nthreads) {
+    const int64_t col = nb * BN + c;
+    if (col >= N) continue;
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       if (m >= M) break;
-      float r[V];
-#pragma unroll
-      for (int e = 0; e < V; ++e) r[e] = 0.f;
-      const float* src = ws + static_cast<int64_t>(m) * N;
-      for (int q0 = 0; q0 < split_k; q0 += kSliceBatch) {
-        float part[kSliceBatch][V];
-#pragma unroll
-        for (int b = 0; b < kSliceBatch; ++b) {
-          const int q = (q0 + b < split_k) ? q0 + b : split_k - 1;
-#pragma unroll
-          for (int e = 0; e < V; ++e) {
-            const int64_t c = (cl + e < N) ? cl + e : N - 1;
-            part[b][e] = __hip_atomic_load(src + static_cast<int64_t>(q) * M * N + c,
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-        }
-#pragma unroll
-        for (int b = 0; b < kSliceBatch; ++b)
-          if (q0 + b < split_k)
-#pragma unroll
-            for (int e = 0; e < V; ++e) r[e] += part[b][e];
-      }
-#pragma unroll
-      for (int e = 0; e < V; ++e) acc[m][e] = r[e];
-    }
-    if (lane == 0)
-      __hip_atomic_store(&tickets[nb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-
-#pragma unroll
-  for (int m = 0; m < MR; ++m) {
-    if (m >= M) break;
-#pragma unroll
-    for (int e = 0; e < V; ++e) {
-      const int64_t c = col0 + e;
-      if (c >= N) continue;
-      float v = acc[m][e];
-      if (epilogue == KF_EPILOGUE_BIAS_GELU) v = gelu_tanh(v + to_f32(bias[c]));
-      y[m * ldy_m + c * ldy_n] = from_f32<T>(v);
+      float r = wave_sum(m, c);
+      if (epilogue == KF_EPILOGUE_BIAS_GELU) r = gelu_tanh(r + to_f32(bias[col]));
+      y[m * ldy_m + col * ldy_n] = from_f32<T>(r);
     }
   }
 }
 
 size_t ticket_bytes(int64_t N) {
-  // One ticket per 64-column strip covers every dtype (strips are >= 64 wide).
-  return static_cast<size_t>((ceil_div(N, 64) * 4 + 255) / 256 * 256);
+  // One ticket per strip; the narrowest strip has kMinStripColumns columns.
+  return static_cast<size_t>((ceil_div(N, kMinStripColumns) * 4 + 255) / 256 * 256);
 }
 
 template <typename T>
 int launch_gemv(const void* x, const void* W, const void* bias, void* y, int64_t M, int64_t N,
                 int64_t K, int64_t ldx_m, int64_t ldx_k, int64_t ldw_k, int64_t ldw_n,
-                int64_t ldy_m, int64_t ldy_n, int epilogue, int split_k, int waves, void* ws,
-                hipStream_t s) {
+                int64_t ldy_m, int64_t ldy_n, int epilogue, int split_k, int waves, int lpr,
+                void* ws, hipStream_t s) {
   constexpr int V = Vec<T>::N;
   const bool vec = ldw_n == 1 && aligned16(W) && (ldw_k * sizeof(T)) % 16 == 0;
-  const dim3 grid(static_cast<unsigned>(ceil_div(N, kWave * V)), static_cast<unsigned>(split_k));
+  const dim3 grid(static_cast<unsigned>(ceil_div(N, static_cast<int64_t>(lpr) * V)),
+                  static_cast<unsigned>(split_k));
   const dim3 block(waves * kWave);
   unsigned* tickets = static_cast<unsigned*>(ws);
   float* partial = ws ? reinterpret_cast<float*>(static_cast<char*>(ws) + ticket_bytes(N)) : nullptr;
-  auto go = [&](auto mr) -> int {
+  auto go = [&](auto mr, auto lanes) -> int {
     constexpr int MR = decltype(mr)::value;
+    constexpr int LPR = decltype(lanes)::value;
     if (waves * kWave > gemv_max_lanes<MR>()) {
       set_error("gemv: register pressure: %d rows allow at most %d waves, got %d", MR,
                 gemv_max_lanes<MR>() / kWave, waves);
       return KF_ERR_OUT_OF_RESOURCES;
     }
-    const size_t lds = static_cast<size_t>(waves) * MR * kWave * V * sizeof(float);
+    const size_t lds = static_cast<size_t>(waves) * MR * LPR * V * sizeof(float);
     if (lds > kGemvMaxLds) {
       set_error("gemv: waves=%d x %d rows needs %zu B of LDS for the wave reduction (limit %zu)",
                 waves, MR, lds, kGemvMaxLds);
       return KF_ERR_OUT_OF_RESOURCES;
     }
-    hipLaunchKernelGGL((gemv_splitk<T, MR>), grid, block, lds, s, static_cast<const T*>(x),
+    hipLaunchKernelGGL((gemv_splitk<T, MR, LPR>), grid, block, lds, s, static_cast<const T*>(x),
                        static_cast<const T*>(W), static_cast<const T*>(bias), static_cast<T*>(y),
                        M, N, K, ldx_m, ldx_k, ldw_k, ldw_n, ldy_m, ldy_n, epilogue, split_k,
                        vec ? 1 : 0, partial, tickets);
     return launch_status("gemv");
   };
-  if (M <= 1) return go(std::integral_constant<int, 1>{});
-  if (M <= 2) return go(std::integral_constant<int, 2>{});
-  if (M <= 4) return go(std::integral_constant<int, 4>{});
-  return go(std::integral_constant<int, 8>{});
+  auto with_rows = [&](auto lanes) -> int {
+    if (M <= 1) return go(std::integral_constant<int, 1>{}, lanes);
+    if (M <= 2) return go(std::integral_constant<int, 2>{}, lanes);
+    if (M <= 4) return go(std::integral_constant<int, 4>{}, lanes);
+    return go(std::integral_constant<int, 8>{}, lanes);
+  };
+  switch (lpr) {
+    case 8: return with_rows(std::integral_constant<int, 8>{});
+    case 16: return with_rows(std::integral_constant<int, 16>{});
+    case 32: return with_rows(std::integral_constant<int, 32>{});
+    default: return with_rows(std::integral_constant<int, 64>{});
+  }
 }
 
 }  // namespace
@@ -269,8 +308,8 @@ extern "C" size_t kf_gemv_workspace_bytes(int64_t M, int64_t N, int split_k) {
 extern "C" int kf_gemv(int dtype, const void* x, const void* W, const void* bias, void* y,
                        int64_t M, int64_t N, int64_t K, int64_t ldx_m, int64_t ldx_k,
                        int64_t ldw_k, int64_t ldw_n, int64_t ldy_m, int64_t ldy_n, int epilogue,
-                       int split_k, int waves, void* workspace, size_t workspace_bytes,
-                       void* stream) {
+                       int split_k, int waves, int lanes_per_row, void* workspace,
+                       size_t workspace_bytes, void* stream) {
   using namespace kf;
   if (M < 0 || N < 0 || K < 0) {
     set_error("gemv: negative shape");
@@ -287,6 +326,10 @@ extern "C" int kf_gemv(int dtype, const void* x, const void* W, const void* bias
   if (waves < 1 || waves > kGemvMaxWaves) {
     set_error("gemv: waves=%d outside 1..%d", waves, kGemvMaxWaves);
     return KF_ERR_OUT_OF_RESOURCES;
+  }
+  if (lanes_per_row != 8 && lanes_per_row != 16 && lanes_per_row != 32 && lanes_per_row != 64) {
+    set_error("gemv: lanes_per_row=%d must be 8, 16, 32 or 64", lanes_per_row);
+    return KF_ERR_INVALID_ARGUMENT;
   }
   if (split_k < 1 || split_k > 65535) {
     set_error("gemv: split_k=%d outside 1..65535", split_k);
@@ -313,13 +356,13 @@ extern "C" int kf_gemv(int dtype, const void* x, const void* W, const void* bias
   switch (dtype) {
     case KF_DTYPE_F32:
       return launch_gemv<float>(x, W, bias, y, M, N, K, ldx_m, ldx_k, ldw_k, ldw_n, ldy_m, ldy_n,
-                                epilogue, split_k, waves, workspace, s);
+                                epilogue, split_k, waves, lanes_per_row, workspace, s);
     case KF_DTYPE_F16:
       return launch_gemv<f16>(x, W, bias, y, M, N, K, ldx_m, ldx_k, ldw_k, ldw_n, ldy_m, ldy_n,
-                              epilogue, split_k, waves, workspace, s);
+                              epilogue, split_k, waves, lanes_per_row, workspace, s);
     case KF_DTYPE_BF16:
       return launch_gemv<bf16>(x, W, bias, y, M, N, K, ldx_m, ldx_k, ldw_k, ldw_n, ldy_m, ldy_n,
-                               epilogue, split_k, waves, workspace, s);
+                               epilogue, split_k, waves, lanes_per_row, workspace, s);
     default:
       set_error("gemv: unsupported dtype code %d", dtype);
       return KF_ERR_UNSUPPORTED_DTYPE;

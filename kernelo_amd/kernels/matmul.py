@@ -22,7 +22,7 @@ from kernelo_amd.runtime import hip
 from kernelo_amd.runtime.env import MI355X_CAPS
 from kernelo_amd.testing import exact_fp32_matmul
 from kernelo_amd.tuning.config import KernelConfig, Problem
-from kernelo_amd.tuning.search import MatmulSearchSpace
+from kernelo_amd.tuning.search import GEMV_DEFAULT_LANES_PER_ROW, MatmulSearchSpace
 
 #: A mid-size tile compiled for every dtype: the fixed, always-feasible
 #: configuration (the reference's DEFAULT_CONFIG, matmul.py:118-120).
@@ -77,6 +77,7 @@ def launch_gemm(
             code, a.data_ptr(), b.data_ptr(), bias_ptr, out.data_ptr(),
             m, n, k, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
             out.stride(0), out.stride(1), epilogue, split, cfg["num_warps"],
+            cfg.get("LANES_PER_ROW", GEMV_DEFAULT_LANES_PER_ROW),
             ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
             stream,
         )
@@ -106,7 +107,8 @@ def matmul(a: torch.Tensor, b: torch.Tensor, *, config: KernelConfig | None = No
 class MatmulOperator(Operator):
     name = "matmul"
     config_order = (
-        "BLOCK_M", "BLOCK_N", "BLOCK_K", "GROUP_M", "DIRECT", "GEMV", "SPLIT_K", "num_warps",
+        "BLOCK_M", "BLOCK_N", "BLOCK_K", "GROUP_M", "DIRECT", "GEMV", "SPLIT_K", "LANES_PER_ROW",
+        "num_warps",
         "num_stages",
     )
 

@@ -109,7 +109,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "kf_gemv": (
         _int,
         [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int,
-         _int, _int, _vp, _sz, _vp],
+         _int, _int, _int, _vp, _sz, _vp],
     ),
     "kf_gemv_workspace_bytes": (_sz, [_i64, _i64, _int]),
     "kf_softmax": (_int, [_int, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _int, _vp]),

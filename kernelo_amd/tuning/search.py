@@ -357,6 +357,16 @@ def gemm_instantiation_reason(
     return None
 
 
+#: Lanes per row segment of a GEMV config that does not name it (the strip
+#: width of the first GEMV, kept so that older cached configs keep their meaning).
+GEMV_DEFAULT_LANES_PER_ROW = 64
+
+
+def gemv_unroll(rows: int) -> int:
+    """Rows of W each lane keeps in flight per trip (gemv.hip gemv_unroll)."""
+    return 16 if rows <= 1 else (8 if rows <= 2 else 4)
+
+
 class _GemmSpace(SearchSpace):
     """Shared by matmul and fused_linear: same main loop, different epilogue."""
 
@@ -375,8 +385,9 @@ class _GemmSpace(SearchSpace):
     GEMV_MAX_M = 8
     SPLIT_K = (1, 2, 4, 8, 16, 32, 64)
     GEMV_WARPS = (1, 2, 4, 8, 16)
-    #: Rows of W each wave keeps in flight per trip (gemv.hip kGemvUnroll).
-    GEMV_UNROLL = 8
+    #: Lanes per row segment: a strip is LANES_PER_ROW 16-byte vectors wide and
+    #: one wave load covers 64 / LANES_PER_ROW rows.
+    GEMV_LANES_PER_ROW = (8, 16, 32, 64)
     #: Dynamic LDS the GEMV wave reduction may use (gemv.hip kGemvMaxLds).
     GEMV_MAX_LDS = 64 * 1024
 
@@ -395,13 +406,16 @@ class _GemmSpace(SearchSpace):
                 num_stages=stages,
             )
         if problem.dims_dict["M"] <= self.GEMV_MAX_M:
-            for split, warps in product(self.SPLIT_K, self.GEMV_WARPS):
-                yield KernelConfig(self.operation, GEMV=1, SPLIT_K=split, num_warps=warps)
+            for split, lanes, warps in product(self.SPLIT_K, self.GEMV_LANES_PER_ROW, self.GEMV_WARPS):
+                yield KernelConfig(
+                    self.operation, GEMV=1, SPLIT_K=split, LANES_PER_ROW=lanes, num_warps=warps
+                )
 
     def num_programs(self, config: KernelConfig, problem: Problem) -> int:
         dims = problem.dims_dict
         if config.get("GEMV"):
-            strip = 64 * (VECTOR_BYTES // problem.itemsize)
+            lanes = config.get("LANES_PER_ROW", GEMV_DEFAULT_LANES_PER_ROW)
+            strip = lanes * (VECTOR_BYTES // problem.itemsize)
             return ceil_div(dims["N"], strip) * config["SPLIT_K"]
         return ceil_div(dims["M"], config["BLOCK_M"]) * ceil_div(dims["N"], config["BLOCK_N"])
 
@@ -436,17 +450,20 @@ class _GemmSpace(SearchSpace):
 
     def _gemv_reason(self, config: KernelConfig, m: int, k: int, elem: int) -> str | None:
         warps, split = config["num_warps"], config["SPLIT_K"]
+        lanes = config.get("LANES_PER_ROW", GEMV_DEFAULT_LANES_PER_ROW)
         mr = next_power_of_2(m)
-        if mr > 4 and warps > 8:
-            return f"register pressure: {mr} rows of x allow at most 8 waves, got {warps}"
-        lds = warps * mr * 64 * (VECTOR_BYTES // elem) * 4
+        max_warps = 16 if mr == 4 else 8
+        if warps > max_warps:
+            return f"register pressure: {mr} rows of x allow at most {max_warps} waves, got {warps}"
+        lds = warps * mr * lanes * (VECTOR_BYTES // elem) * 4
         if lds > self.GEMV_MAX_LDS:
             return f"LDS: wave reduction needs {lds // 1024} KiB at num_warps={warps}, M={m}"
         slice_rows = ceil_div(k, split)
-        if split > 1 and slice_rows < warps * self.GEMV_UNROLL:
+        in_flight = warps * (64 // lanes) * gemv_unroll(mr)
+        if split > 1 and slice_rows < in_flight:
             return (
                 f"split-K slice too short: {slice_rows} rows of K for {warps} waves x "
-                f"{self.GEMV_UNROLL} rows in flight"
+                f"{64 // lanes} rows x {gemv_unroll(mr)} in flight"
             )
         return None
 
@@ -462,20 +479,22 @@ class _GemmSpace(SearchSpace):
         flight, and its 8-wave form (two waves per SIMD hide LDS latency);
         register-staged tiles prefer fewer waves (more registers each).
         GEMV: HBM-bound, so (1) at least one workgroup per CU, (2) at least
-        eight waves per CU (each keeps 8 x 1 KiB row segments in flight, and
-        HBM needs ~32 KiB in flight per CU), then fewer slices (less partial-sum
-        traffic) and fewer waves. GEMV candidates sort ahead of MFMA tiles for
-        decode shapes.
+        four waves per CU (each keeps 16 x 16 bytes per lane in flight, and
+        HBM needs ~32 KiB in flight per CU), then fewer slices (a shorter
+        cross-slice tail), 16-lane row segments, and fewer waves. GEMV
+        candidates sort ahead of MFMA tiles for decode shapes.
         """
         dims = problem.dims_dict
         programs = self.num_programs(config, problem)
         if config.get("GEMV"):
             waves = programs * config["num_warps"]
+            lanes = config.get("LANES_PER_ROW", GEMV_DEFAULT_LANES_PER_ROW)
             return (
                 0,
                 -min(programs, caps.cu_count),
-                -min(waves, 8 * caps.cu_count),
+                -min(waves, 4 * caps.cu_count),
                 config["SPLIT_K"],
+                abs(lanes.bit_length() - 5),  # 16 lanes per row measured best
                 config["num_warps"],
             )
         bm, bn = config["BLOCK_M"], config["BLOCK_N"]

@@ -49,7 +49,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_identification(lib):
-    assert lib.kf_abi_version() == 1
+    assert lib.kf_abi_version() == 2
     assert lib.kf_build_target() == b"gfx950"
 
 
@@ -71,7 +71,7 @@ def test_variant_table_equals_the_instantiation_rules(lib):
 
 def test_workspace_sizing(lib):
     assert lib.kf_gemv_workspace_bytes(1, 11008, 1) == 0
-    tickets = (-(-11008 // 64) * 4 + 255) // 256 * 256
+    tickets = (-(-11008 // 32) * 4 + 255) // 256 * 256  # one per strip; strips >= 32 columns
     assert lib.kf_gemv_workspace_bytes(1, 11008, 8) == tickets + 8 * 11008 * 4
     assert lib.kf_gemv_workspace_bytes(0, 11008, 8) == 0
 
@@ -109,14 +109,16 @@ def test_gemm_argument_errors(lib):
 
 
 def test_gemv_argument_errors(lib):
-    def gemv(m=1, n=64, k=64, split=1, waves=4, ws=NULL, wsb=0, dtype=2, epi=0):
+    def gemv(m=1, n=64, k=64, split=1, waves=4, ws=NULL, wsb=0, dtype=2, epi=0, lanes=16):
         return lib.kf_gemv(dtype, 1 << 20, 1 << 20, NULL, 1 << 20, m, n, k, k, 1, n, 1, n, 1, epi,
-                           split, waves, ws, wsb, NULL)
+                           split, waves, lanes, ws, wsb, NULL)
 
     rc, msg = _rc_and_message(lambda: gemv(m=9))
     assert rc == hip.KF_ERR_INVALID_ARGUMENT and "decode limit" in msg
     rc, msg = _rc_and_message(lambda: gemv(waves=17))
     assert rc == hip.KF_ERR_OUT_OF_RESOURCES
+    rc, msg = _rc_and_message(lambda: gemv(lanes=12))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "lanes_per_row" in msg
     rc, msg = _rc_and_message(lambda: gemv(split=0))
     assert rc == hip.KF_ERR_INVALID_ARGUMENT and "split_k" in msg
     rc, msg = _rc_and_message(lambda: gemv(split=4))

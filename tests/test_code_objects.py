@@ -45,7 +45,7 @@ def test_every_kernel_is_present(kernels):
     assert len(gemm) == n_gemm
     assert sum("softmax_rows" in n for n in kernels) == 3 * 7
     assert sum("rmsnorm_rows" in n for n in kernels) == 3 * 7
-    assert sum("gemv_splitk" in n for n in kernels) == 3 * 4
+    assert sum("gemv_splitk" in n for n in kernels) == 3 * 4 * 4  # dtypes x row counts x strip widths
 
 
 def test_no_kernel_spills_to_scratch(kernels):

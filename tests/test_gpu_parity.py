@@ -14,6 +14,7 @@ import pytest
 import torch
 
 from kernelo_amd.benchmark.workloads import MATMUL_SHAPES, ROW_SHAPES
+from kernelo_amd.runtime import hip
 from kernelo_amd.testing import verify
 from kernelo_amd.tuning.config import KernelConfig
 from oracle import ops
@@ -276,16 +277,28 @@ def test_fused_linear_zero_weight_is_gelu_of_bias():
 # --- Decode GEMV -----------------------------------------------------------------
 
 
-@pytest.mark.parametrize("split", (1, 2, 8, 16, 64))
-@pytest.mark.parametrize("warps", (1, 4, 8, 16))
-def test_gemv_decode_config(split, warps):
-    """BASELINE config 5a: bf16 1x11008x4096, U(-1, 1)."""
+def test_gemv_single_row_caps_the_workgroup_at_eight_waves():
+    """One x row keeps 16 rows of W in flight per lane: 512 lanes at most."""
+    from kernelo_amd.kernels.matmul import matmul
+
+    x = torch.ones(1, 256, dtype=torch.bfloat16, device=DEV)
+    w = torch.ones(256, 512, dtype=torch.bfloat16, device=DEV)
+    cfg = KernelConfig("matmul", GEMV=1, SPLIT_K=1, LANES_PER_ROW=16, num_warps=16)
+    with pytest.raises(hip.KernelOutOfResources, match="at most 8 waves"):
+        matmul(x, w, config=cfg)
+
+
+@pytest.mark.parametrize("split", (1, 2, 4, 8, 16, 64))
+@pytest.mark.parametrize("warps", (1, 4, 8))
+@pytest.mark.parametrize("lanes", (8, 16, 32, 64))
+def test_gemv_decode_config(split, warps, lanes):
+    """BASELINE config 5a: bf16 1x11008x4096, U(-1, 1), every strip width."""
     from kernelo_amd.kernels.matmul import matmul
 
     g = torch.Generator().manual_seed(0)
     x = (torch.rand(1, 4096, generator=g) * 2 - 1).to(torch.bfloat16)
     w = (torch.rand(4096, 11008, generator=g) * 2 - 1).to(torch.bfloat16)
-    cfg = KernelConfig("matmul", GEMV=1, SPLIT_K=split, num_warps=warps)
+    cfg = KernelConfig("matmul", GEMV=1, SPLIT_K=split, LANES_PER_ROW=lanes, num_warps=warps)
     out = matmul(x.to(DEV), w.to(DEV), config=cfg)
     _gate(ops.matmul_ref(x, w), out, torch.bfloat16, str(cfg))
 
@@ -295,7 +308,7 @@ def test_gemv_is_deterministic():
 
     x = _randn(1, 4096, dtype=torch.bfloat16, seed=1).to(DEV)
     w = _randn(4096, 11008, dtype=torch.bfloat16, seed=2).to(DEV)
-    cfg = KernelConfig("matmul", GEMV=1, SPLIT_K=32, num_warps=8)
+    cfg = KernelConfig("matmul", GEMV=1, SPLIT_K=32, LANES_PER_ROW=16, num_warps=8)
     first = matmul(x, w, config=cfg)
     for _ in range(5):
         assert torch.equal(matmul(x, w, config=cfg), first)
@@ -303,12 +316,13 @@ def test_gemv_is_deterministic():
 
 @pytest.mark.parametrize("m", (1, 2, 3, 5, 8))
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
-def test_gemv_small_batches(m, dtype):
+@pytest.mark.parametrize("lanes", (8, 16, 64))
+def test_gemv_small_batches(m, dtype, lanes):
     from kernelo_amd.kernels.matmul import matmul
 
     x = _randn(m, 1000, dtype=dtype, seed=m)
     w = _randn(1000, 3000, dtype=dtype, seed=9, scale=1000**-0.5)
-    cfg = KernelConfig("matmul", GEMV=1, SPLIT_K=4, num_warps=4)
+    cfg = KernelConfig("matmul", GEMV=1, SPLIT_K=4, LANES_PER_ROW=lanes, num_warps=4)
     out = matmul(x.to(DEV), w.to(DEV), config=cfg)
     _gate(ops.matmul_ref(x, w), out, dtype, f"gemv m={m}")
 
@@ -339,7 +353,8 @@ def _guarded_call(m, n, k, cfg, seed, dtype=torch.bfloat16):
         ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=DEV)
         rc = lib.kf_gemv(abi_code(dtype), da.data_ptr(), db.data_ptr(), None, cptr, m, n, k,
                          da.stride(0), da.stride(1), db.stride(0), db.stride(1), pitch, 1, 0,
-                         cfg["SPLIT_K"], cfg["num_warps"], ws.data_ptr(), ws.numel(), stream)
+                         cfg["SPLIT_K"], cfg["num_warps"], cfg.get("LANES_PER_ROW", 64),
+                         ws.data_ptr(), ws.numel(), stream)
     else:
         rc = lib.kf_gemm(abi_code(dtype), da.data_ptr(), db.data_ptr(), None, cptr, m, n, k,
                          da.stride(0), da.stride(1), db.stride(0), db.stride(1), pitch, 1, 0,
@@ -366,6 +381,9 @@ def _guarded_call(m, n, k, cfg, seed, dtype=torch.bfloat16):
         (777, 1032, 328, KernelConfig("matmul", BLOCK_M=256, BLOCK_N=128, BLOCK_K=64, GROUP_M=8, DIRECT=1, num_warps=8, num_stages=2)),
         (1, 7, 3, KernelConfig("matmul", GEMV=1, SPLIT_K=1, num_warps=1)),
         (1, 7, 3, KernelConfig("matmul", GEMV=1, SPLIT_K=2, num_warps=4)),
+        (1, 7, 3, KernelConfig("matmul", GEMV=1, SPLIT_K=2, LANES_PER_ROW=8, num_warps=4)),
+        (3, 1000, 301, KernelConfig("matmul", GEMV=1, SPLIT_K=3, LANES_PER_ROW=16, num_warps=4)),
+        (8, 1032, 127, KernelConfig("matmul", GEMV=1, SPLIT_K=2, LANES_PER_ROW=32, num_warps=8)),
         (1, 7, 3, KernelConfig("matmul", BLOCK_M=32, BLOCK_N=32, BLOCK_K=32, GROUP_M=8, num_warps=4, num_stages=2)),
     ],
     ids=lambda v: str(v) if not isinstance(v, KernelConfig) else "-".join(f"{x}" for x in v.values()),

@@ -160,20 +160,42 @@ def test_budget_is_honoured():
 
 @pytest.mark.parametrize("m", [1, 2, 4, 8])
 def test_decode_shapes_offer_split_k_gemv_first(m):
-    cands = MatmulSearchSpace().candidates(_gemm(m, 11008, 4096, "bf16"), MI355X_CAPS)
+    space = MatmulSearchSpace()
+    problem = _gemm(m, 11008, 4096, "bf16")
+    cands = space.candidates(problem, MI355X_CAPS)
     assert cands and cands[0].get("GEMV") == 1
-    assert any(c.get("GEMV") is None for c in cands)  # MFMA tiles stay in the running
+    # MFMA tiles stay feasible; the budget may be spent on GEMV configs alone.
+    every = MatmulSearchSpace(max_candidates=10_000).candidates(problem, MI355X_CAPS)
+    assert any(c.get("GEMV") is None for c in every)
+    first_tile = next(i for i, c in enumerate(every) if c.get("GEMV") is None)
+    assert all(c.get("GEMV") == 1 for c in every[:first_tile])
 
 
 def test_gemv_rules():
     space = MatmulSearchSpace()
     problem = _gemm(1, 4096, 256, "bf16")
-    short = KernelConfig("matmul", GEMV=1, SPLIT_K=64, num_warps=16)
+    # 8 waves x 4 rows (16 lanes per row) x 16 in flight = 512 rows > 256 / 64.
+    short = KernelConfig("matmul", GEMV=1, SPLIT_K=64, LANES_PER_ROW=16, num_warps=8)
     assert "split-K slice too short" in space.reject_reason(short, problem, MI355X_CAPS)
-    wide = KernelConfig("matmul", GEMV=1, SPLIT_K=1, num_warps=16)
+    wide = KernelConfig("matmul", GEMV=1, SPLIT_K=1, LANES_PER_ROW=64, num_warps=16)
     assert "register pressure" in space.reject_reason(wide, _gemm(8, 4096, 4096, "bf16"), MI355X_CAPS)
-    big = KernelConfig("matmul", GEMV=1, SPLIT_K=1, num_warps=8)
+    assert "register pressure" in space.reject_reason(wide, _gemm(1, 4096, 4096, "bf16"), MI355X_CAPS)
+    four = KernelConfig("matmul", GEMV=1, SPLIT_K=1, LANES_PER_ROW=16, num_warps=16)
+    assert space.reject_reason(four, _gemm(4, 4096, 4096, "bf16"), MI355X_CAPS) is None
+    # LDS for the wave reduction: waves x rows x strip columns x 4 bytes.
+    big = KernelConfig("matmul", GEMV=1, SPLIT_K=1, LANES_PER_ROW=64, num_warps=8)
     assert "LDS" in space.reject_reason(big, _gemm(8, 4096, 4096, "bf16"), MI355X_CAPS)
+    narrow = KernelConfig("matmul", GEMV=1, SPLIT_K=1, LANES_PER_ROW=16, num_warps=8)
+    assert space.reject_reason(narrow, _gemm(8, 4096, 4096, "bf16"), MI355X_CAPS) is None
+
+
+def test_gemv_strip_width_sets_the_workgroup_count():
+    space = MatmulSearchSpace()
+    problem = _gemm(1, 11008, 4096, "bf16")
+    cfg = KernelConfig("matmul", GEMV=1, SPLIT_K=4, LANES_PER_ROW=16, num_warps=4)
+    assert space.num_programs(cfg, problem) == 86 * 4  # 128-column strips
+    legacy = KernelConfig("matmul", GEMV=1, SPLIT_K=8, num_warps=16)  # no LANES_PER_ROW: 64
+    assert space.num_programs(legacy, problem) == 22 * 8
 
 
 def test_no_gemv_candidates_above_eight_rows():
@@ -182,7 +204,7 @@ def test_no_gemv_candidates_above_eight_rows():
 
 
 def test_overshoot_rule_keeps_the_smallest_tile():
-    result = MatmulSearchSpace().generate(_gemm(1, 11008, 4096), MI355X_CAPS)
+    result = MatmulSearchSpace(max_candidates=10_000).generate(_gemm(1, 11008, 4096), MI355X_CAPS)
     tiles = [c for c in result.candidates if not c.get("GEMV")]
     assert tiles and all(c["BLOCK_M"] == 32 for c in tiles)
 
