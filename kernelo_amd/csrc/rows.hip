@@ -107,6 +107,17 @@ struct RowTile {
   }
 };
 
+// Barrier for the LDS exchange only: this wave's LDS accesses are complete
+// (lgkmcnt(0)) and the compiler may not move memory operations across it. It
+// does not wait for outstanding global stores (the fences of __syncthreads()
+// would): the previous row's stores stay in flight across the reductions.
+__device__ __forceinline__ void lds_sync() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt/expcnt unconstrained
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Workgroup reduction: wave64 butterfly, then one LDS exchange. `slot`
 // alternates between two buffers so a reduction needs a single barrier: the
 // buffer reused two reductions later cannot be overwritten before every wave
@@ -119,7 +130,7 @@ __device__ __forceinline__ float block_reduce(float x, float (*part)[kMaxWaves],
   const int wave = threadIdx.x / kWave;
   if (nwaves == 1) return x;
   if (lane == 0) part[slot][wave] = x;
-  __syncthreads();
+  lds_sync();
   float r = part[slot][0];
   for (int w = 1; w < nwaves; ++w) r = IsMax ? fmaxf(r, part[slot][w]) : r + part[slot][w];
   slot ^= 1;

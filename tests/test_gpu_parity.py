@@ -395,3 +395,47 @@ def test_edge_shapes_guard_band(m, n, k, cfg):
     assert guard_ok, "kernel wrote outside C"
     assert torch.isfinite(inside).all()
     _gate(ops.matmul_ref(a, b).float(), inside, torch.bfloat16, f"{cfg} {m}x{n}x{k}")
+
+
+# --- HIP graph capture -------------------------------------------------------------
+
+
+def test_graph_replays_match_eager_results():
+    """Every kernel family captured into one HIP graph (as bench.py times them):
+    three replays, with eager work and synchronisations in between, each
+    bitwise equal to the eager results. The split-K GEMV's ticket counters are
+    reset by the kernel itself, so replays need no memset node."""
+    from kernelo_amd.kernels.fused_linear import fused_linear_gelu
+    from kernelo_amd.kernels.matmul import matmul
+    from kernelo_amd.kernels.rmsnorm import rmsnorm
+    from kernelo_amd.kernels.softmax import softmax
+
+    a = _randn(300, 520, dtype=torch.float16, seed=1).to(DEV)
+    b = _randn(520, 264, dtype=torch.float16, seed=2).to(DEV)
+    bias = _randn(264, dtype=torch.float16, seed=3).to(DEV)
+    x = _randn(1, 4096, dtype=torch.bfloat16, seed=4).to(DEV)
+    w = _randn(4096, 1024, dtype=torch.bfloat16, seed=5, scale=4096**-0.5).to(DEV)
+    r = _randn(64, 1000, dtype=torch.float32, seed=6).to(DEV)
+    gamma = _randn(1000, dtype=torch.float32, seed=7).to(DEV)
+    direct = KernelConfig("matmul", BLOCK_M=128, BLOCK_N=128, BLOCK_K=64, GROUP_M=8, DIRECT=1,
+                          num_warps=8, num_stages=3)
+    gemv = KernelConfig("matmul", GEMV=1, SPLIT_K=8, LANES_PER_ROW=16, num_warps=4)
+
+    def run():
+        return [matmul(a, b, config=direct), fused_linear_gelu(a, b, bias),
+                matmul(x, w, config=gemv), rmsnorm(r, gamma), softmax(r)]
+
+    eager = run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = run()
+    for _ in range(3):
+        for t in captured:
+            t.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, want in zip(captured, eager):
+            assert torch.equal(got, want)
+        _ = run()  # eager work between replays
+        torch.cuda.synchronize()
