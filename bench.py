@@ -144,6 +144,8 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-sustained", action="store_true",
+                        help="skip the graph-captured sustained runs (profiling the headline method)")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(
@@ -191,7 +193,10 @@ def main(argv: list[str] | None = None) -> int:
         flushed = _time_flushed(fns[0], steps, warmup, flush)
         mean_ms = float(np.mean(flushed))
         rate = (work / (mean_ms * 1e-3)) / scale
-        sustained_ms, dev = _time_graph(fns, steps, warmup, flush)
+        if args.no_sustained:
+            sustained_ms, dev = float("nan"), 0.0
+        else:
+            sustained_ms, dev = _time_graph(fns, steps, warmup, flush)
         if dev != 0.0:
             raise RuntimeError(f"{name}: graph replay differs from the eager result by {dev:.3g}")
         entry = {
@@ -281,7 +286,7 @@ def main(argv: list[str] | None = None) -> int:
                   metrics.matmul_flops(M, N, K), "TFLOP/s", f16_peak, src)
     tg = _time_flushed(lambda: torch.matmul(a, b), steps, warmup, flush)
     gemm["torch_hipblaslt_tflops"] = metrics.matmul_flops(M, N, K) / (np.mean(tg) * 1e-3) / 1e12
-    ms, _ = _time_graph([lambda c=c: torch.matmul(c[0], c[1]) for c in cp], steps, warmup, flush)
+    ms, _ = (float("nan"), 0.0) if args.no_sustained else _time_graph([lambda c=c: torch.matmul(c[0], c[1]) for c in cp], steps, warmup, flush)
     gemm["torch_hipblaslt_sustained_tflops"] = metrics.matmul_flops(M, N, K) / (ms * 1e-3) / 1e12
     del cp
 
@@ -300,7 +305,7 @@ def main(argv: list[str] | None = None) -> int:
     tu = _time_flushed(lambda: linear_gelu_reference(fx, fw, fb), steps, warmup, flush)
     fused["unfused_torch_3op_us"] = float(np.mean(tu)) * 1e3
     fused["speedup_vs_unfused"] = fused["unfused_torch_3op_us"] / fused["mean_us"]
-    ms, _ = _time_graph([lambda c=c: linear_gelu_reference(c[0], c[1], c[2]) for c in cp],
+    ms, _ = (float("nan"), 0.0) if args.no_sustained else _time_graph([lambda c=c: linear_gelu_reference(c[0], c[1], c[2]) for c in cp],
                         steps, warmup, flush)
     fused["unfused_torch_3op_sustained_us"] = ms * 1e3
     del fx, fw, cp
@@ -318,7 +323,7 @@ def main(argv: list[str] | None = None) -> int:
                   work, "GB/s", hbm, src)
     tv = _time_flushed(lambda: torch.matmul(vx, vw), steps, warmup, flush)
     gemv["torch_gbps"] = work / (np.mean(tv) * 1e-3) / 1e9
-    ms, _ = _time_graph([lambda c=c: torch.matmul(c[0], c[1]) for c in cp], steps, warmup, flush)
+    ms, _ = (float("nan"), 0.0) if args.no_sustained else _time_graph([lambda c=c: torch.matmul(c[0], c[1]) for c in cp], steps, warmup, flush)
     gemv["torch_sustained_gbps"] = work / (ms * 1e-3) / 1e9
     del cp
 
