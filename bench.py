@@ -5,7 +5,9 @@
 A "step" is one launch of a kernel over one batch of synthetic input that is
 already resident in HBM. Every BASELINE configuration is measured; the
 headline ``value`` is configuration 3, the fp16 GEMM 2048x4096x4096 in
-TFLOP/s (BASELINE.json ``metric``).
+TFLOP/s (BASELINE.json ``metric``). Two further lines cover the kernels
+added beyond the BASELINE set: vector_add over 2^26 fp32 elements (the HBM
+probe) and the two-pass RMSNorm on fp16 rows of 32768.
 
 Timing, as the reference measures (kernelforge/benchmark/runner.py:169-183):
 for each of the K steps, flush L2 + Infinity Cache, record a start event,
@@ -327,6 +329,38 @@ def main(argv: list[str] | None = None) -> int:
     gemv["torch_sustained_gbps"] = work / (ms * 1e-3) / 1e9
     del cp
 
+    # --- widened rows: vector_add (the HBM probe) and the two-pass RMSNorm --------
+    from kernelo_amd.kernels.vector_add import vector_add
+
+    VN = 1 << 26
+    va = torch.randn(VN, generator=g).to(dev)
+    vb = torch.randn(VN, generator=g).to(dev)
+    acfg, src = pick("vector_add", "fp32", n=VN)
+    assert torch.equal(vector_add(va, vb, config=acfg), va + vb), "vector_add must be bit-exact"
+    work = metrics.vector_add_bytes(VN, 4)
+    r, cp = copies_of(work, va, vb)
+    vadd = record("vector_add_fp32_67108864",
+                  [lambda c=c: vector_add(c[0], c[1], config=acfg) for c in cp],
+                  work, "GB/s", hbm, src)
+    ta = _time_flushed(lambda: va + vb, steps, warmup, flush)
+    vadd["torch_gbps"] = work / (np.mean(ta) * 1e-3) / 1e9
+    del cp, va, vb
+
+    WR, WC = 4096, 32768
+    wx = torch.randn(WR, WC, generator=g).to(torch.float16).to(dev)
+    wg = (1.0 + 0.1 * torch.randn(WC, generator=g)).to(torch.float16).to(dev)
+    wcfg, src = pick("rmsnorm", "fp16", rows=WR, cols=WC)
+    assert_verified(rmsnorm_reference(wx, wg, eps=1e-6), rmsnorm(wx, wg, eps=1e-6, config=wcfg),
+                    context="two-pass rmsnorm")
+    work = metrics.rmsnorm_bytes(WR, WC, 2)
+    r, cp = copies_of(work, wx, wg)
+    wide = record(f"rmsnorm_two_pass_fp16_{WR}x{WC}",
+                  [lambda c=c: rmsnorm(c[0], c[1], eps=1e-6, config=wcfg) for c in cp],
+                  work, "GB/s", hbm, src)
+    tw = _time_flushed(lambda: rmsnorm_reference(wx, wg, eps=1e-6), steps, warmup, flush)
+    wide["torch_eager_gbps"] = work / (np.mean(tw) * 1e-3) / 1e9
+    del cp
+
     # --- CPU baseline: the oracle on the host cores, bounded slices ----------------
     # About 4 s of calls per workload (about 20 s in all), on bounded slices of the
     # same inputs; the headline is the GEMM slice.
@@ -366,6 +400,15 @@ def main(argv: list[str] | None = None) -> int:
         results["fused_linear_fp16_4096x11008x4096"]["cpu_baseline"] = cpu_entry(
             lambda: ops.linear_gelu_ref(fxs, fws, fbs), metrics.matmul_flops(64, FN, FK), "TFLOP/s",
             f"oracle linear_gelu_ref on X[:64], 64x{FN}x{FK}")
+        ca2 = torch.randn(1 << 22, generator=g)
+        cb2 = torch.randn(1 << 22, generator=g)
+        results["vector_add_fp32_67108864"]["cpu_baseline"] = cpu_entry(
+            lambda: ops.vector_add_ref(ca2, cb2), metrics.vector_add_bytes(1 << 22, 4), "GB/s",
+            "oracle vector_add_ref on 4194304 fp32 elements")
+        cwx, cwg = wx[:64].cpu(), wg.cpu()
+        results[f"rmsnorm_two_pass_fp16_{WR}x{WC}"]["cpu_baseline"] = cpu_entry(
+            lambda: ops.rmsnorm_ref(cwx, cwg, 1e-6), metrics.rmsnorm_bytes(64, WC, 2), "GB/s",
+            f"oracle rmsnorm_ref on x[:64], 64x{WC} fp16")
 
     line = {
         "metric": METRIC,

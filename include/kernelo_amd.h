@@ -149,6 +149,34 @@ int kf_rmsnorm(int dtype, const void* x, const void* gamma, void* y, int64_t row
                int64_t cols, int64_t x_row_stride, int64_t y_row_stride, float eps,
                int block_size, int rows_per_program, int waves, void* stream);
 
+/*
+ * Two-pass RMSNorm for rows of any width: the reference's first listed future
+ * improvement (README.md:656-660), which lifts the single-pass cap of
+ * kf_rmsnorm. Same math, rounding and argument meaning as kf_rmsnorm except:
+ *   block_size : columns per trip of the workgroup over its row, a multiple
+ *                of waves*64*(16 / element size) -- 1, 2, 4 or 8 16-byte
+ *                vectors per lane per trip;
+ *   stage_row  : 1 keeps the row in LDS between the passes (one HBM read),
+ *                which needs cols*element size <= the value
+ *                kf_rmsnorm_two_pass_max_staged_cols() reports; 0 reads the
+ *                row twice.
+ */
+int kf_rmsnorm_two_pass(int dtype, const void* x, const void* gamma, void* y, int64_t rows,
+                        int64_t cols, int64_t x_row_stride, int64_t y_row_stride, float eps,
+                        int block_size, int rows_per_program, int waves, int stage_row,
+                        void* stream);
+/* Widest row (in elements of `dtype`) that kf_rmsnorm_two_pass can stage in LDS. */
+int64_t kf_rmsnorm_two_pass_max_staged_cols(int dtype);
+
+/*
+ * Elementwise c[i] = a[i] + b[i] over n contiguous elements, fp32 sum rounded
+ * once. Replaces vector_add() (kernels/vector_add.py:43-57): a workgroup of
+ * `waves` wavefronts owns block_size elements (block_size / (waves*64) per
+ * lane, a power of two from 1 to 64).
+ */
+int kf_vector_add(int dtype, const void* a, const void* b, void* c, int64_t n, int block_size,
+                  int waves, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

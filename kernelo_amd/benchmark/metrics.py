@@ -21,6 +21,11 @@ def elementwise_bytes(elements: int, itemsize: int, *, tensors: int) -> int:
     return elements * itemsize * tensors
 
 
+def vector_add_bytes(n: int, itemsize: int) -> int:
+    """Read a and b, write c."""
+    return elementwise_bytes(n, itemsize, tensors=3)
+
+
 def rmsnorm_bytes(rows: int, cols: int, itemsize: int) -> int:
     """Read x, write y, read gamma once per launch."""
     return (2 * rows * cols + cols) * itemsize

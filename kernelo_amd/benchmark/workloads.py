@@ -1,9 +1,10 @@
 """Named problem suites.
 
 The shape lists are the reference's (kernelforge/benchmark/workloads.py:
-26-136): a Llama-7B-sized transformer (hidden 4096, MLP 11008), decode and
-prefill token counts, and a ``correctness`` suite of awkward shapes -- 1s,
-primes and off-by-one tile boundaries -- that exercises every masked tail.
+26-136; the vector_add counts at :108-113): a Llama-7B-sized transformer
+(hidden 4096, MLP 11008), decode and prefill token counts, and a
+``correctness`` suite of awkward shapes -- 1s, primes and off-by-one tile
+boundaries -- that exercises every masked tail.
 """
 
 from __future__ import annotations
@@ -79,6 +80,16 @@ ROW_SHAPES: dict[str, tuple[tuple[int, int], ...]] = {
     ),
 }
 
+#: vector_add element counts: a prime just over a million and a 32 MiB fp16
+#: stream for smoke; powers of four for the sweep; one prefill activation;
+#: and counts around every tile boundary for correctness.
+VECTOR_SHAPES: dict[str, tuple[int, ...]] = {
+    "smoke": (1_000_003, 16_777_216),
+    "sweep": (1 << 16, 1 << 20, 1 << 24, 1 << 26),
+    "transformer": (TOKEN_COUNTS[-1] * HIDDEN,),
+    "correctness": (1, 2, 13, 127, 128, 129, 1024, 12_345, 1_000_003, 1 << 20),
+}
+
 SUITES: tuple[str, ...] = ("smoke", "sweep", "transformer", "correctness")
 
 
@@ -92,4 +103,6 @@ def problems(operation: str, suite: str = "sweep", dtype: str | torch.dtype = "f
         return [
             Problem.create(operation, dtype, rows=rows, cols=cols) for rows, cols in ROW_SHAPES[suite]
         ]
+    if operation == "vector_add":
+        return [Problem.create(operation, dtype, n=n) for n in VECTOR_SHAPES[suite]]
     raise ValueError(f"no workload suite defined for {operation!r}")

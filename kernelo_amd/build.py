@@ -110,6 +110,8 @@ def build(jobs: int | None = None, verbose: bool = True) -> Path:
         (CSRC / "abi.hip", obj_dir / "abi.o", []),
         (CSRC / "rows.hip", obj_dir / "rows.o", []),
         (CSRC / "gemv.hip", obj_dir / "gemv.o", []),
+        (CSRC / "wide_rows.hip", obj_dir / "wide_rows.o", []),
+        (CSRC / "elementwise.hip", obj_dir / "elementwise.o", []),
         (CSRC / "gemm.hip", obj_dir / "gemm.o", []),
     ]
     for dt, combo, c, inc in units:

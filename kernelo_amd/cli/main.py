@@ -1,18 +1,28 @@
-"""Command line interface: ``kernelo_amd env|tune|cache|profile``.
+"""Command line interface:
+``kernelo_amd env|tune|benchmark|compare|profile|report|cache``.
 
 Every subcommand is a thin wrapper over a library call (kernelforge/cli/
-main.py): ``tune`` over :class:`~kernelo_amd.tuning.tuner.Tuner`, ``cache``
-over :class:`~kernelo_amd.tuning.cache.ConfigCache`, ``profile`` over the
-launch-count attribution and a single-launch mode that ``rocprofv3`` wraps for
-hardware counters. Exit codes: 0 success, 1 failure (including no candidate
-passing the gate), 2 unusable environment; errors print ``error: ...`` to
-stderr.
+main.py:23-643):
+
+* ``tune`` over :class:`~kernelo_amd.tuning.tuner.Tuner`;
+* ``benchmark`` runs a named workload suite (``benchmark.workloads``) through
+  dispatch, the gate and the timer and records every row in the database;
+* ``compare`` times every implementation at one shape, or a whole
+  :class:`~kernelo_amd.integration.TransformerBlock` per backend;
+* ``profile`` attributes launches, or makes the single launch that
+  ``rocprofv3 --pmc`` wraps for hardware counters;
+* ``report`` renders ``summary.md``, CSV and figures from the database;
+* ``cache`` lists or clears the winner cache.
+
+Exit codes: 0 success, 1 failure (including no candidate passing the gate),
+2 unusable environment; errors print ``error: ...`` to stderr.
 """
 
 from __future__ import annotations
 
 import argparse
 import sys
+from pathlib import Path
 
 from kernelo_amd import __version__
 from kernelo_amd.dtypes import SUPPORTED_DTYPES, parse_dtype
@@ -23,7 +33,9 @@ _ROW_OPERATIONS = ("rmsnorm", "softmax")
 _DEFAULT_GEMM = {"m": 2048, "n": 4096, "k": 4096}
 _DEFAULT_ROW = {"rows": 4096, "cols": 4096}
 
-OPERATIONS = (*_GEMM_OPERATIONS, *_ROW_OPERATIONS)
+_DEFAULT_ELEMENTS = 1 << 24
+
+OPERATIONS = (*_GEMM_OPERATIONS, *_ROW_OPERATIONS, "vector_add")
 
 
 def _rule(title: str) -> str:
@@ -47,6 +59,8 @@ def build_problem(operation: str, args: argparse.Namespace) -> Problem:
             rows=args.rows or _DEFAULT_ROW["rows"],
             cols=args.cols or _DEFAULT_ROW["cols"],
         )
+    if operation == "vector_add":
+        return Problem.create(operation, dtype, n=args.elements or _DEFAULT_ELEMENTS)
     raise ValueError(f"unknown operation {operation!r}")
 
 
@@ -205,6 +219,201 @@ def command_tune(args: argparse.Namespace) -> int:
     return 0 if result.best is not None else 1
 
 
+# --- benchmark -----------------------------------------------------------------
+def _rate(operator, problem, median_ms: float) -> tuple[str, float | None, float | None]:
+    """Headline rate text plus the (tflops, gbps) pair to record."""
+    from kernelo_amd.benchmark import metrics
+
+    if operator.is_memory_bound():
+        value = metrics.gbps(operator.bytes_moved(problem), median_ms)
+        return f"{value:.1f} GB/s", None, value
+    value = metrics.tflops(operator.flops(problem), median_ms)
+    return f"{value:.1f} TFLOP/s", value, None
+
+
+def _cpu_runnable(operator, inputs):
+    """torch eager on host copies of the inputs: the ``torch_cpu`` baseline."""
+    host = tuple(t.detach().to("cpu") for t in inputs)
+    return lambda: operator.reference(*host)
+
+
+def command_benchmark(args: argparse.Namespace) -> int:
+    from kernelo_amd.benchmark import workloads
+    from kernelo_amd.benchmark.runner import benchmark
+    from kernelo_amd.db import Measurement
+    from kernelo_amd.kernels import get_operator
+    from kernelo_amd.runtime.dispatch import select_config
+    from kernelo_amd.runtime.env import capture_environment, require_gpu
+    from kernelo_amd.testing import exact_fp32_matmul, verify
+
+    device = require_gpu()
+    operator = get_operator(args.operation)
+    problems = workloads.problems(args.operation, args.suite, args.dtype)
+    environment = capture_environment(device)
+    cache = _open_cache(args)
+    db = _open_db(args)
+    run_id = (
+        db.start_run(environment, notes=f"benchmark:{args.suite}", version=__version__)
+        if db is not None
+        else None
+    )
+    print(environment.render())
+    print(_rule(f"{args.operation} / {args.suite} / {args.dtype}"))
+    header = f"{'shape':<24}{'impl':<14}{'config':<10}{'median ms':>11}{'p99 ms':>10}{'metric':>16}"
+    print(header)
+    print("-" * len(header))
+    failures = 0
+    try:
+        for problem in problems:
+            inputs = operator.make_inputs(problem, device)
+            with exact_fp32_matmul():
+                reference = operator.reference(*inputs)
+                selection = select_config(operator, problem, cache=cache, device=device)
+                runnable = dict(operator.baselines(problem, inputs))
+                runnable["kernelo_amd"] = lambda c=selection.config, i=inputs: operator.run(c, *i)
+                if args.cpu_baseline:
+                    runnable["torch_cpu"] = _cpu_runnable(operator, inputs)
+                for label, fn in runnable.items():
+                    source = selection.source if label == "kernelo_amd" else "-"
+                    try:
+                        out = fn()
+                        check = verify(reference, out.to(reference.device), dtype=problem.dtype)
+                    except Exception as exc:  # noqa: BLE001 - reported per row, never fatal
+                        failures += label == "kernelo_amd"
+                        print(f"{problem.shape_key:<24}{label:<14}{source:<10}  failed: "
+                              f"{type(exc).__name__}: {str(exc)[:80]}")
+                        if db is not None:
+                            db.record(run_id, problem, Measurement(
+                                label=label, status="runtime_error",
+                                config=selection.config if label == "kernelo_amd" else None,
+                                error=f"{type(exc).__name__}: {exc}"))
+                        continue
+                    if not check.passed:
+                        failures += label == "kernelo_amd"
+                        print(f"{problem.shape_key:<24}{label:<14}{source:<10}  INCORRECT: "
+                              f"{check.reason}")
+                        if db is not None:
+                            db.record(run_id, problem, Measurement(
+                                label=label, status="incorrect", verification=check,
+                                config=selection.config if label == "kernelo_amd" else None))
+                        continue
+                    on_host = label == "torch_cpu"
+                    timing = benchmark(
+                        fn,
+                        warmup=min(args.warmup, 1) if on_host else args.warmup,
+                        iterations=min(args.iterations, 3) if on_host else args.iterations,
+                        device="cpu" if on_host else device,
+                        flush_l2=not args.no_flush_l2 and not on_host,
+                    )
+                    text, tflops_value, gbps_value = _rate(operator, problem, timing.median_ms)
+                    print(f"{problem.shape_key:<24}{label:<14}{source:<10}"
+                          f"{timing.median_ms:>11.4f}{timing.p99_ms:>10.4f}{text:>16}")
+                    if db is not None:
+                        db.record(run_id, problem, Measurement(
+                            label=label, status="ok",
+                            config=selection.config if label == "kernelo_amd" else None,
+                            verification=check, timing=timing, tflops=tflops_value,
+                            gbps=gbps_value))
+    finally:
+        if db is not None:
+            db.close()
+    return 1 if failures else 0
+
+
+# --- compare -------------------------------------------------------------------
+def command_compare(args: argparse.Namespace) -> int:
+    if args.operation == "transformer":
+        return _compare_transformer(args)
+
+    from kernelo_amd.benchmark.runner import benchmark
+    from kernelo_amd.kernels import get_operator
+    from kernelo_amd.runtime.dispatch import select_config
+    from kernelo_amd.runtime.env import require_gpu
+    from kernelo_amd.testing import exact_fp32_matmul, verify
+
+    device = require_gpu()
+    operator = get_operator(args.operation)
+    problem = build_problem(args.operation, args)
+    print(_describe_problem(problem))
+    inputs = operator.make_inputs(problem, device)
+    with exact_fp32_matmul():
+        reference = operator.reference(*inputs)
+        selection = select_config(operator, problem, cache=_open_cache(args), device=device)
+        print(f"config: {selection.describe()}")
+        print(f"        {', '.join(f'{k}={v}' for k, v in selection.config.items())}")
+        runnable = dict(operator.baselines(problem, inputs))
+        runnable["kernelo_amd"] = lambda: operator.run(selection.config, *inputs)
+        print(_rule("Comparison"))
+        rows = []
+        for label, fn in runnable.items():
+            check = verify(reference, fn(), dtype=problem.dtype)
+            if not check.passed:
+                print(f"{label}: INCORRECT ({check.reason})")
+                continue
+            timing = benchmark(
+                fn, warmup=args.warmup, iterations=args.iterations, device=device,
+                flush_l2=not args.no_flush_l2,
+            )
+            rows.append((label, timing, check))
+    rows.sort(key=lambda row: row[1].median_ms)
+    eager = next((t.median_ms for label, t, _ in rows if label == "torch_eager"), None)
+    header = f"{'impl':<14}{'median ms':>11}{'p99 ms':>10}{'vs eager':>10}{'metric':>16}{'max err':>11}"
+    print(header)
+    print("-" * len(header))
+    for label, timing, check in rows:
+        text, _, _ = _rate(operator, problem, timing.median_ms)
+        relative = f"{eager / timing.median_ms:.2f}x" if eager else "-"
+        print(f"{label:<14}{timing.median_ms:>11.4f}{timing.p99_ms:>10.4f}{relative:>10}"
+              f"{text:>16}{check.error:>11.2e}")
+    return 0
+
+
+def _compare_transformer(args: argparse.Namespace) -> int:
+    from kernelo_amd.integration import BlockConfig, benchmark_block
+    from kernelo_amd.runtime.env import require_gpu
+
+    device = require_gpu()
+    config = BlockConfig(hidden=args.hidden, heads=args.heads, intermediate=args.intermediate)
+    print(
+        f"Transformer block: hidden={config.hidden} heads={config.heads} "
+        f"intermediate={config.intermediate} batch={args.batch} seq={args.seq} dtype={args.dtype}"
+    )
+    results = benchmark_block(
+        config, batch=args.batch, seq=args.seq, dtype=parse_dtype(args.dtype), device=device,
+        warmup=args.warmup, iterations=args.iterations, cache=_open_cache(args),
+    )
+    print(_rule("Block latency"))
+    baseline = results["torch"].median_ms
+    for backend, timing in results.items():
+        ratio = "" if backend == "torch" else f"  ({baseline / timing.median_ms:.3f}x)"
+        print(f"{backend:<14}{timing.median_ms:>10.3f} ms{ratio}")
+    print(
+        "\nOnly the two RMSNorms and the MLP up-projection with its bias + GELU are swapped;\n"
+        "attention and the other projections are PyTorch in both, so the block-level\n"
+        "speedup is bounded by the share of block time those operators held."
+    )
+    return 0
+
+
+# --- report --------------------------------------------------------------------
+def command_report(args: argparse.Namespace) -> int:
+    from kernelo_amd.benchmark import report
+    from kernelo_amd.db import ResultsDB
+
+    path = Path(args.db)
+    if not path.exists():
+        print(f"no results database at {path}; run `kernelo_amd tune` first.", file=sys.stderr)
+        return 2
+    with ResultsDB(path) as db:
+        counts = db.counts()
+        print(
+            f"{counts['results']} measurements across {counts['problems']} problems "
+            f"and {counts['runs']} runs"
+        )
+        print(report.generate(db, args.out).render())
+    return 0
+
+
 # --- profile -------------------------------------------------------------------
 def command_profile(args: argparse.Namespace) -> int:
     from kernelo_amd.kernels import get_operator
@@ -262,6 +471,7 @@ def _add_shape_arguments(parser: argparse.ArgumentParser) -> None:
     group.add_argument("-k", "--k", type=int, help="GEMM reduction size (matmul, fused_linear)")
     group.add_argument("--rows", type=int, help="rows (rmsnorm, softmax)")
     group.add_argument("--cols", type=int, help="row width (rmsnorm, softmax)")
+    group.add_argument("--elements", type=int, help="element count (vector_add)")
 
 
 def _add_measurement_arguments(parser: argparse.ArgumentParser, *, warmup=25, iterations=200):
@@ -309,6 +519,32 @@ def build_parser() -> argparse.ArgumentParser:
         help="print the candidate-generation breakdown and exit without tuning",
     )
 
+    bench = sub.add_parser("benchmark", help="run a named workload suite")
+    bench.add_argument("operation", choices=OPERATIONS)
+    bench.add_argument("--suite", default="sweep", choices=("smoke", "sweep", "transformer"))
+    _add_measurement_arguments(bench, iterations=100)
+    _add_storage_arguments(bench)
+    bench.add_argument(
+        "--cpu-baseline",
+        action="store_true",
+        help="also time torch eager on the host cores (label torch_cpu; 3 iterations)",
+    )
+
+    compare = sub.add_parser(
+        "compare", help="compare implementations at one shape, or a whole transformer block"
+    )
+    compare.add_argument("operation", choices=(*OPERATIONS, "transformer"))
+    _add_shape_arguments(compare)
+    _add_measurement_arguments(compare, iterations=100)
+    _add_storage_arguments(compare)
+    compare.add_argument("--batch", type=int, default=1, help="transformer: batch size")
+    compare.add_argument("--seq", type=int, default=2048, help="transformer: sequence length")
+    compare.add_argument("--hidden", type=int, default=4096, help="transformer: hidden size")
+    compare.add_argument("--heads", type=int, default=32, help="transformer: attention heads")
+    compare.add_argument(
+        "--intermediate", type=int, default=11008, help="transformer: MLP intermediate size"
+    )
+
     profile = sub.add_parser("profile", help="attribute device time and launches to kernels")
     profile.add_argument("operation", choices=OPERATIONS)
     _add_shape_arguments(profile)
@@ -322,6 +558,10 @@ def build_parser() -> argparse.ArgumentParser:
         "the target for `rocprofv3 --pmc ... -- kernelo_amd profile ... --backend launch-once`",
     )
 
+    report = sub.add_parser("report", help="render tables and figures from the database")
+    _add_storage_arguments(report)
+    report.add_argument("--out", default="reports", help="output directory")
+
     cache = sub.add_parser("cache", help="inspect or clear the tuned-config cache")
     cache.add_argument("cache_command", choices=("list", "clear"))
     _add_storage_arguments(cache)
@@ -331,7 +571,10 @@ def build_parser() -> argparse.ArgumentParser:
 _COMMANDS = {
     "env": command_env,
     "tune": command_tune,
+    "benchmark": command_benchmark,
+    "compare": command_compare,
     "profile": command_profile,
+    "report": command_report,
     "cache": command_cache,
 }
 

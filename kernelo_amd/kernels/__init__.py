@@ -14,6 +14,7 @@ if TYPE_CHECKING:
     from kernelo_amd.kernels.base import Operator
 
 _OPERATORS: dict[str, tuple[str, str]] = {
+    "vector_add": ("kernelo_amd.kernels.vector_add", "VectorAddOperator"),
     "softmax": ("kernelo_amd.kernels.softmax", "SoftmaxOperator"),
     "matmul": ("kernelo_amd.kernels.matmul", "MatmulOperator"),
     "rmsnorm": ("kernelo_amd.kernels.rmsnorm", "RMSNormOperator"),
@@ -21,6 +22,7 @@ _OPERATORS: dict[str, tuple[str, str]] = {
 }
 
 _FUNCTIONS: dict[str, str] = {
+    "vector_add": "kernelo_amd.kernels.vector_add",
     "matmul": "kernelo_amd.kernels.matmul",
     "fused_linear_gelu": "kernelo_amd.kernels.fused_linear",
     "softmax": "kernelo_amd.kernels.softmax",

@@ -1,4 +1,4 @@
-"""Single-pass RMSNorm on gfx950: ``y = x * rsqrt(mean(x^2) + eps) * gamma``.
+"""RMSNorm on gfx950: ``y = x * rsqrt(mean(x^2) + eps) * gamma``.
 
 Python surface of the reference's ``rmsnorm`` (kernelforge/kernels/rmsnorm.py:
 38-206), which also replaces its handwritten CUDA kernel
@@ -6,6 +6,13 @@ Python surface of the reference's ``rmsnorm`` (kernelforge/kernels/rmsnorm.py:
 and the gamma multiply are fp32 and the result is rounded once, so the fp16
 sum-of-squares precision trap (rmsnorm.py:16-25) cannot occur. ``eps`` sits
 inside the root, keeping an all-zero row finite.
+
+Two kernels sit behind it. The single-pass kernel holds a row in registers
+(up to 16384 values); a config with ``TWO_PASS=1`` selects the two-pass
+kernel, which walks a row of any width twice, optionally parking it in LDS
+in between (``STAGE_ROW=1``). The two-pass kernel is the reference's first
+listed future improvement (README.md:656-660); the default configuration
+uses it for rows beyond the single-pass limit.
 """
 
 from __future__ import annotations
@@ -25,8 +32,8 @@ from kernelo_amd.tuning.search import RMSNormSearchSpace, default_row_config
 DEFAULT_EPS = 1e-5
 
 
-def default_config(n_cols: int) -> KernelConfig:
-    return default_row_config("rmsnorm", n_cols)
+def default_config(n_cols: int, dtype: torch.dtype | None = None) -> KernelConfig:
+    return default_row_config("rmsnorm", n_cols, dtype)
 
 
 def rmsnorm(
@@ -51,7 +58,9 @@ def rmsnorm(
         raise ValueError("gamma must be contiguous")
     if gamma.dtype != x.dtype:
         raise ValueError(f"dtype mismatch: {x.dtype} vs {gamma.dtype}")
-    cfg = config or default_config(n_cols)
+    cfg = config or default_config(n_cols, x.dtype)
+    if cfg.get("TWO_PASS"):
+        return _rmsnorm_two_pass(x, gamma, float(eps), cfg)
     _check_row_config(cfg, n_cols, RMSNormSearchSpace.MAX_BLOCK_SIZE, "hidden size")
     out = torch.empty_like(x, memory_format=torch.contiguous_format)
     hip.require_device_tensor(x, gamma)
@@ -66,6 +75,23 @@ def rmsnorm(
     return out
 
 
+def _rmsnorm_two_pass(
+    x: torch.Tensor, gamma: torch.Tensor, eps: float, cfg: KernelConfig
+) -> torch.Tensor:
+    n_rows, n_cols = x.shape
+    out = torch.empty_like(x, memory_format=torch.contiguous_format)
+    hip.require_device_tensor(x, gamma)
+    lib = hip.load()
+    rc = lib.kf_rmsnorm_two_pass(
+        abi_code(x.dtype), x.data_ptr(), gamma.data_ptr(), out.data_ptr(), n_rows, n_cols,
+        x.stride(0) if n_rows > 1 else n_cols, out.stride(0) if n_rows > 1 else n_cols,
+        eps, cfg["BLOCK_SIZE"], cfg["ROWS_PER_PROGRAM"], cfg["num_warps"],
+        int(cfg.get("STAGE_ROW", 0)), hip.stream_of(x),
+    )
+    hip.check(rc, "rmsnorm_two_pass")
+    return out
+
+
 def rmsnorm_reference(
     x: torch.Tensor, gamma: torch.Tensor, *, eps: float = DEFAULT_EPS
 ) -> torch.Tensor:
@@ -77,7 +103,7 @@ def rmsnorm_reference(
 
 class RMSNormOperator(Operator):
     name = "rmsnorm"
-    config_order = ("BLOCK_SIZE", "ROWS_PER_PROGRAM", "num_warps")
+    config_order = ("TWO_PASS", "BLOCK_SIZE", "ROWS_PER_PROGRAM", "STAGE_ROW", "num_warps")
 
     def __init__(self, eps: float = DEFAULT_EPS) -> None:
         self.eps = eps
@@ -105,7 +131,7 @@ class RMSNormOperator(Operator):
         return rmsnorm(x, gamma, eps=self.eps, config=config)
 
     def default_config(self, problem: Problem) -> KernelConfig:
-        return default_config(problem.dims_dict["cols"])
+        return default_config(problem.dims_dict["cols"], problem.dtype)
 
     def flops(self, problem: Problem) -> int:
         d = problem.dims_dict
@@ -125,5 +151,7 @@ class RMSNormOperator(Operator):
         cols = problem.dims_dict["cols"]
         return {
             "torch_eager": lambda: rmsnorm_reference(x, gamma, eps=self.eps),
-            "hip_default": lambda: rmsnorm(x, gamma, eps=self.eps, config=default_config(cols)),
+            "hip_default": lambda: rmsnorm(
+                x, gamma, eps=self.eps, config=default_config(cols, problem.dtype)
+            ),
         }

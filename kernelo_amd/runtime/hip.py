@@ -117,6 +117,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _int,
         [_int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _int, _int, _int, _vp],
     ),
+    "kf_rmsnorm_two_pass": (
+        _int,
+        [_int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _int, _int, _int, _int,
+         _vp],
+    ),
+    "kf_rmsnorm_two_pass_max_staged_cols": (_i64, [_int]),
+    "kf_vector_add": (_int, [_int, _vp, _vp, _vp, _i64, _int, _int, _vp]),
 }
 
 _lock = threading.Lock()

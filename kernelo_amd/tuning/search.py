@@ -617,18 +617,163 @@ class SoftmaxSearchSpace(_RowReductionSpace):
     operation = "softmax"
 
 
+#: Bytes of a row the two-pass RMSNorm may keep in LDS between its passes:
+#: 160 KiB per workgroup on gfx950 less room for the reduction buffer
+#: (csrc/wide_rows.hip, kMaxStagedBytes).
+TWO_PASS_MAX_STAGED_BYTES = 159 * 1024
+
+
+def two_pass_block(warps: int, unroll: int, elem: int) -> int:
+    """Columns one trip of the two-pass RMSNorm covers: a 16-byte vector per
+    lane, ``unroll`` times."""
+    return warps * 64 * (VECTOR_BYTES // elem) * unroll
+
+
 class RMSNormSearchSpace(_RowReductionSpace):
+    """The single-pass grid plus the two-pass kernel as an algorithmic axis.
+
+    The reference lists the two-pass variant as its first future improvement
+    (README.md:656-660): it lifts the 16384-column cap and gives the space a
+    choice of algorithm, not only of tuning. A two-pass point is
+    ``TWO_PASS=1`` with BLOCK_SIZE = columns per trip (``TWO_PASS_UNROLL``
+    16-byte vectors per lane), and ``STAGE_ROW`` = 1 to keep the row in LDS
+    between the passes so HBM sees it once.
+    """
+
     operation = "rmsnorm"
+    TWO_PASS_WARPS = (4, 8, 16)
+    TWO_PASS_UNROLL = (1, 2, 4, 8)
+    TWO_PASS_ROWS_PER_PROGRAM = (1, 2, 4)
+    STAGE_ROW = (1, 0)
+
+    def grid(self, problem: Problem) -> Iterator[KernelConfig]:
+        yield from super().grid(problem)
+        elem = itemsize(problem.dtype)
+        for warps, unroll, rows, stage in product(
+            self.TWO_PASS_WARPS, self.TWO_PASS_UNROLL, self.TWO_PASS_ROWS_PER_PROGRAM,
+            self.STAGE_ROW,
+        ):
+            yield KernelConfig(
+                self.operation,
+                TWO_PASS=1,
+                BLOCK_SIZE=two_pass_block(warps, unroll, elem),
+                ROWS_PER_PROGRAM=rows,
+                STAGE_ROW=stage,
+                num_warps=warps,
+            )
+
+    def reject_reason(self, config: KernelConfig, problem: Problem, caps: DeviceCaps) -> str | None:
+        if not config.get("TWO_PASS"):
+            return super().reject_reason(config, problem, caps)
+        d = problem.dims_dict
+        elem = itemsize(problem.dtype)
+        warps = config["num_warps"]
+        lanes = warps * caps.wave_size
+        if lanes > caps.max_threads_per_workgroup:
+            return f"workgroup size: {lanes} lanes exceeds {caps.max_threads_per_workgroup}"
+        unroll = config["BLOCK_SIZE"] // two_pass_block(warps, 1, elem)
+        # x and gamma for `unroll` vectors per lane: 8 of each need more than
+        # the 128 registers a lane has at 16 waves.
+        if unroll >= 8 and warps > 8:
+            return f"register pressure: {unroll} vectors per lane allow at most 8 waves, got {warps}"
+        row_bytes = d["cols"] * elem
+        if config.get("STAGE_ROW") and row_bytes > TWO_PASS_MAX_STAGED_BYTES:
+            return (
+                f"LDS: a staged row of {row_bytes // 1024} KiB exceeds "
+                f"{TWO_PASS_MAX_STAGED_BYTES // 1024} KiB"
+            )
+        smallest = two_pass_block(min(self.TWO_PASS_WARPS), 1, elem)
+        if config["BLOCK_SIZE"] > max(next_power_of_2(d["cols"]), smallest):
+            return f"idle lanes: a trip of {config['BLOCK_SIZE']} columns for a row of {d['cols']}"
+        if config["ROWS_PER_PROGRAM"] > d["rows"]:
+            return f"ROWS_PER_PROGRAM={config['ROWS_PER_PROGRAM']} exceeds {d['rows']} rows"
+        return None
+
+    def priority(
+        self, config: KernelConfig, problem: Problem, caps: DeviceCaps
+    ) -> tuple[float, ...]:
+        """Single-pass first where it fits (it reads the row once, from
+        registers); two-pass after it, staged rows first, then 2-4 vectors in
+        flight per lane."""
+        if not config.get("TWO_PASS"):
+            return (0, *super().priority(config, problem, caps))
+        programs = min(self.num_programs(config, problem), caps.cu_count)
+        unroll = config["BLOCK_SIZE"] // two_pass_block(config["num_warps"], 1, itemsize(problem.dtype))
+        return (
+            1, -programs, -config.get("STAGE_ROW", 0), abs(unroll - 3), -config["num_warps"],
+            config["ROWS_PER_PROGRAM"],
+        )
 
 
-def default_row_config(operation: str, n_cols: int) -> KernelConfig:
-    """One wave per 512 columns, up to 16 waves; one row per workgroup."""
+def default_row_config(operation: str, n_cols: int, dtype=None) -> KernelConfig:
+    """One wave per 512 columns, up to 16 waves; one row per workgroup.
+
+    For RMSNorm rows beyond the single-pass limit: the two-pass kernel at 8
+    waves and 8192 columns per trip (valid for every dtype: four fp32 or two
+    16-bit vectors per lane), with the row staged in LDS when it fits there
+    at ``dtype``'s width (fp32 when no dtype is given).
+    """
     block = next_power_of_2(n_cols)
+    if operation == "rmsnorm" and block > _RowReductionSpace.MAX_BLOCK_SIZE:
+        elem = itemsize(dtype) if dtype is not None else 4
+        return KernelConfig(
+            operation,
+            TWO_PASS=1,
+            BLOCK_SIZE=8192,
+            ROWS_PER_PROGRAM=1,
+            STAGE_ROW=int(n_cols * elem <= TWO_PASS_MAX_STAGED_BYTES),
+            num_warps=8,
+        )
     warps = max(1, min(_RowReductionSpace.MAX_WAVES, block // 512))
     return KernelConfig(operation, BLOCK_SIZE=block, ROWS_PER_PROGRAM=1, num_warps=warps)
 
 
+class VectorAddSearchSpace(SearchSpace):
+    """Elementwise: nothing to tile or reuse (search.py:514-539 in the reference).
+
+    BLOCK_SIZE elements per workgroup of ``num_warps`` waves; a lane holds
+    BLOCK_SIZE / lanes of them, a power of two from 1 to 64 (the compiled
+    set), loaded 16 bytes at a time where that many fit.
+    """
+
+    operation = "vector_add"
+    BLOCK_SIZE = (256, 512, 1024, 2048, 4096, 8192, 16384)
+    NUM_WARPS = (1, 2, 4, 8, 16)
+    MAX_ELEMS_PER_LANE = 64
+
+    def grid(self, problem: Problem) -> Iterator[KernelConfig]:
+        for block, warps in product(self.BLOCK_SIZE, self.NUM_WARPS):
+            yield KernelConfig(self.operation, BLOCK_SIZE=block, num_warps=warps)
+
+    def num_programs(self, config: KernelConfig, problem: Problem) -> int:
+        return ceil_div(problem.dims_dict["n"], config["BLOCK_SIZE"])
+
+    def reject_reason(self, config: KernelConfig, problem: Problem, caps: DeviceCaps) -> str | None:
+        lanes = config["num_warps"] * caps.wave_size
+        if lanes > caps.max_threads_per_workgroup:
+            return f"workgroup size: {lanes} lanes exceeds {caps.max_threads_per_workgroup}"
+        per_lane = config["BLOCK_SIZE"] / lanes
+        if per_lane < 1:
+            return f"idle lanes: {lanes} lanes for BLOCK_SIZE={config['BLOCK_SIZE']}"
+        if per_lane > self.MAX_ELEMS_PER_LANE:
+            return f"register pressure: {per_lane:.0f} elements per lane"
+        return None
+
+    def priority(
+        self, config: KernelConfig, problem: Problem, caps: DeviceCaps
+    ) -> tuple[float, ...]:
+        """Fill the CUs, then whole 16-byte loads, then 64 bytes per lane and
+        operand (four loads of each input in flight), then larger workgroups."""
+        programs = min(self.num_programs(config, problem), caps.cu_count)
+        lane_bytes = config["BLOCK_SIZE"] // (config["num_warps"] * caps.wave_size) * itemsize(
+            problem.dtype
+        )
+        partial = 1 if lane_bytes < VECTOR_BYTES else 0
+        return (-programs, partial, abs(lane_bytes.bit_length() - 7), -config["num_warps"])
+
+
 SEARCH_SPACES: dict[str, type[SearchSpace]] = {
+    "vector_add": VectorAddSearchSpace,
     "softmax": SoftmaxSearchSpace,
     "matmul": MatmulSearchSpace,
     "rmsnorm": RMSNormSearchSpace,

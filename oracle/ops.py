@@ -18,8 +18,13 @@ linear_gelu_ref        linear_gelu_reference: gelu(x@w + bias, approximate="tanh
                        (kernelforge/kernels/fused_linear.py:160-162)
 softmax_ref            SoftmaxOperator.reference: torch.softmax(x, dim=-1)
                        (kernelforge/kernels/softmax.py:124-126)
-rmsnorm_ref            rmsnorm_reference (kernelforge/kernels/rmsnorm.py:130-143)
+rmsnorm_ref            rmsnorm_reference (kernelforge/kernels/rmsnorm.py:130-143);
+                       also the oracle of the two-pass kernel for rows of any
+                       width (the same function, README.md:656-660)
+vector_add_ref         VectorAddOperator.reference: a + b
+                       (kernelforge/kernels/vector_add.py:85-87)
 *_fp64                 textbook definitions evaluated in float64 with numpy
+vector_add_exact       the correctly rounded sum from exact rational arithmetic
 =====================  ===========================================================
 
 How each is pinned (tests/test_oracle.py): against the fp64 definitions on
@@ -27,6 +32,9 @@ small shapes, against closed forms the reference's tests use (constant-row
 softmax = 1/n, identity/zero-weight GELU, all-zero RMSNorm row), against the
 committed golden vectors in tests/golden/, and with planted mistakes (a
 dropped bias, a wrong GELU constant, a transposed operand) that must fail.
+vector_add_ref is pinned bit for bit against vector_add_exact (Fractions,
+round half to even) on random and adversarial 16-bit pairs, and against the
+closed forms a + 0 = a, a + (-a) = +0 and a + b = b + a.
 
 The oracle computes in fp32 with one final rounding to the output dtype,
 which is the contract the HIP kernels implement (fp32 accumulate, single
@@ -79,6 +87,11 @@ def rmsnorm_ref(x: torch.Tensor, gamma: torch.Tensor, eps: float = 1e-5) -> torc
     return (xf * inv_rms * _f32(gamma)).to(x.dtype)
 
 
+def vector_add_ref(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """``a + b`` formed in fp32 and rounded once to the input dtype."""
+    return (_f32(a) + _f32(b)).to(a.dtype)
+
+
 # --- fp64 textbook definitions (small shapes only) ----------------------------
 
 
@@ -127,3 +140,60 @@ def rmsnorm_fp64(x: torch.Tensor, gamma: torch.Tensor, eps: float = 1e-5) -> np.
         ms = sum(v * v for v in X[r]) / X.shape[1]
         out[r] = X[r] / math.sqrt(ms + eps) * G
     return out
+
+
+def _round_to_format(q, mantissa_bits: int, min_exp: int, max_exp: int) -> float:
+    """Nearest value of a binary format to the rational ``q``, ties to even.
+
+    The format has ``mantissa_bits`` fraction bits, normal exponents
+    ``min_exp..max_exp`` and subnormals below; overflow gives +-inf.
+    """
+    from fractions import Fraction
+
+    if q == 0:
+        return 0.0
+    sign = -1.0 if q < 0 else 1.0
+    q = abs(Fraction(q))
+    exp = q.numerator.bit_length() - q.denominator.bit_length()
+    if Fraction(2) ** exp > q:
+        exp -= 1
+    exp = max(exp, min_exp)  # subnormals share the smallest exponent's spacing
+    ulp = Fraction(2) ** (exp - mantissa_bits)
+    units = q / ulp
+    n = units.numerator // units.denominator
+    rem = units - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    value = n * ulp
+    largest = (2 - Fraction(2) ** -mantissa_bits) * Fraction(2) ** max_exp
+    if value > largest:
+        return sign * math.inf
+    return sign * float(value)
+
+
+#: (fraction bits, smallest normal exponent, largest exponent) per dtype.
+_FORMATS = {torch.float16: (10, -14, 15), torch.bfloat16: (7, -126, 127)}
+
+
+def vector_add_exact(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """The exact sum of each pair, rounded to nearest-even in the 16-bit
+    input format: the IEEE definition of the correctly rounded addition,
+    computed with Python Fractions (small inputs only)."""
+    from fractions import Fraction
+
+    fmt = _FORMATS[a.dtype]
+    av = a.detach().to("cpu", torch.float64).reshape(-1).tolist()
+    bv = b.detach().to("cpu", torch.float64).reshape(-1).tolist()
+    out = []
+    for x, y in zip(av, bv):
+        if math.isinf(x) or math.isinf(y) or math.isnan(x) or math.isnan(y):
+            out.append(x + y)
+            continue
+        exact = Fraction(x) + Fraction(y)
+        if exact == 0:
+            # An exact zero sum is +0 under round-to-nearest, except -0 + -0.
+            both_negative = math.copysign(1.0, x) < 0 and math.copysign(1.0, y) < 0
+            out.append(-0.0 if both_negative else 0.0)
+            continue
+        out.append(_round_to_format(exact, *fmt))
+    return torch.tensor(out, dtype=torch.float64).reshape(a.shape).to(a.dtype)

@@ -38,6 +38,7 @@ def test_header_declares_the_expected_entry_points():
         "kf_abi_version", "kf_build_target", "kf_last_error",
         "kf_gemm", "kf_gemm_has_variant", "kf_gemm_variant_count", "kf_gemm_variant_info",
         "kf_gemv", "kf_gemv_workspace_bytes", "kf_softmax", "kf_rmsnorm",
+        "kf_rmsnorm_two_pass", "kf_rmsnorm_two_pass_max_staged_cols", "kf_vector_add",
     }
 
 
@@ -49,7 +50,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_identification(lib):
-    assert lib.kf_abi_version() == 2
+    assert lib.kf_abi_version() == 3
     assert lib.kf_build_target() == b"gfx950"
 
 
@@ -152,6 +153,57 @@ def test_row_kernel_argument_errors(lib):
     rc = lib.kf_rmsnorm(1, 1 << 20, 1 << 20, 1 << 20, 4, 100, 100, 100, ctypes.c_float(-1.0), 128,
                         1, 1, NULL)
     assert rc == hip.KF_ERR_INVALID_ARGUMENT and "eps" in hip.last_error()
+
+
+def test_two_pass_rmsnorm_argument_errors(lib):
+    def two_pass(cols=100_000, block=2048, rpp=1, waves=8, rows=4, dtype=0, stage=0, eps=1e-5):
+        return lib.kf_rmsnorm_two_pass(dtype, 1 << 20, 1 << 20, 1 << 20, rows, cols, cols, cols,
+                                       ctypes.c_float(eps), block, rpp, waves, stage, NULL)
+
+    # fp32: 4 elements per 16-byte vector, so a trip is a multiple of waves*64*4.
+    rc, msg = _rc_and_message(lambda: two_pass(block=1024))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "16-byte vectors per lane" in msg
+    rc, msg = _rc_and_message(lambda: two_pass(block=3 * 2048))
+    assert rc == hip.KF_ERR_NOT_BUILT and "vectors per lane per trip" in msg
+    rc, msg = _rc_and_message(lambda: two_pass(waves=17, block=17 * 256))
+    assert rc == hip.KF_ERR_OUT_OF_RESOURCES
+    rc, msg = _rc_and_message(lambda: two_pass(waves=16, block=16 * 256 * 8))
+    assert rc == hip.KF_ERR_OUT_OF_RESOURCES and "register pressure" in msg
+    rc, msg = _rc_and_message(lambda: two_pass(stage=2))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "stage_row" in msg
+    rc, msg = _rc_and_message(lambda: two_pass(eps=-1.0))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "eps" in msg
+    rc, msg = _rc_and_message(lambda: two_pass(rpp=0))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT
+    rc, msg = _rc_and_message(lambda: two_pass(dtype=5))
+    assert rc == hip.KF_ERR_UNSUPPORTED_DTYPE
+    # The staged row must fit the LDS a workgroup may hold.
+    fp32_cols = lib.kf_rmsnorm_two_pass_max_staged_cols(0)
+    assert fp32_cols == 159 * 1024 // 4
+    assert lib.kf_rmsnorm_two_pass_max_staged_cols(1) == 2 * fp32_cols
+    assert lib.kf_rmsnorm_two_pass_max_staged_cols(7) == 0
+    rc, msg = _rc_and_message(lambda: two_pass(cols=fp32_cols + 4, stage=1))
+    assert rc == hip.KF_ERR_OUT_OF_RESOURCES and "LDS" in msg
+    assert two_pass(rows=0) == hip.KF_OK and two_pass(cols=0) == hip.KF_OK
+
+
+def test_vector_add_argument_errors(lib):
+    def vadd(n=1000, block=1024, waves=4, dtype=1):
+        return lib.kf_vector_add(dtype, 1 << 20, 1 << 20, 1 << 20, n, block, waves, NULL)
+
+    rc, msg = _rc_and_message(lambda: vadd(n=-1))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "negative" in msg
+    rc, msg = _rc_and_message(lambda: vadd(block=100))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "per lane" in msg
+    rc, msg = _rc_and_message(lambda: vadd(block=768, waves=4))
+    assert rc == hip.KF_ERR_NOT_BUILT and "elements per lane" in msg
+    rc, msg = _rc_and_message(lambda: vadd(block=64 * 256, waves=2))
+    assert rc == hip.KF_ERR_NOT_BUILT
+    rc, msg = _rc_and_message(lambda: vadd(waves=0))
+    assert rc == hip.KF_ERR_OUT_OF_RESOURCES
+    rc, msg = _rc_and_message(lambda: vadd(dtype=3))
+    assert rc == hip.KF_ERR_UNSUPPORTED_DTYPE
+    assert vadd(n=0) == hip.KF_OK
 
 
 def test_check_maps_codes_to_tuner_classified_exceptions():

@@ -117,19 +117,37 @@ def test_row_kernel_validation_messages():
         rmsnorm(torch.ones(2, 8), torch.ones(7))
     with pytest.raises(ValueError, match="gamma must be contiguous"):
         rmsnorm(torch.ones(2, 8), torch.ones(8, 2)[:, 0])
+    single_pass = KernelConfig("rmsnorm", BLOCK_SIZE=32768, ROWS_PER_PROGRAM=1, num_warps=16)
     with pytest.raises(ValueError, match="single-pass limit"):
+        rmsnorm(torch.ones(2, 16385), torch.ones(16385), config=single_pass)
+    # Without a config, a row past the limit takes the two-pass kernel, which
+    # still refuses host tensors before anything reaches the library.
+    with pytest.raises(ValueError, match="ROCm device tensor"):
         rmsnorm(torch.ones(2, 16385), torch.ones(16385))
     with pytest.raises(ValueError, match="ROCm device tensor"):
         rmsnorm(torch.ones(2, 8), torch.ones(8))
 
 
+def test_vector_add_validation_messages():
+    from kernelo_amd.kernels.vector_add import vector_add
+
+    a = torch.zeros(8, dtype=torch.float16)
+    with pytest.raises(ValueError, match="shape mismatch"):
+        vector_add(a, torch.zeros(9, dtype=torch.float16))
+    with pytest.raises(ValueError, match="dtype mismatch"):
+        vector_add(a, torch.zeros(8, dtype=torch.float32))
+    with pytest.raises(ValueError, match="ROCm device tensor"):
+        vector_add(a, a)
+
+
 def test_registry_is_lazy_and_named():
     from kernelo_amd.kernels import get_operator, operator_names
 
-    assert set(operator_names()) == {"softmax", "matmul", "rmsnorm", "fused_linear"}
+    assert set(operator_names()) == {"vector_add", "softmax", "matmul", "rmsnorm", "fused_linear"}
     assert get_operator("rmsnorm").name == "rmsnorm"
+    assert get_operator("vector_add").is_memory_bound()
     with pytest.raises(ValueError, match="unknown operator"):
-        get_operator("vector_add")
+        get_operator("layernorm")
 
 
 def test_operators_draw_inputs_on_the_cpu_reproducibly():
@@ -187,6 +205,27 @@ def test_cli_parser_defaults():
     args = build_parser().parse_args(["tune", "rmsnorm"])
     p = build_problem("rmsnorm", args)
     assert p.dims_dict == {"rows": 4096, "cols": 4096} and p.dtype_name == "fp16"
+    args = build_parser().parse_args(["tune", "vector_add", "--elements", "1000003"])
+    assert build_problem("vector_add", args).dims_dict == {"n": 1000003}
+    args = build_parser().parse_args(["benchmark", "softmax", "--suite", "smoke"])
+    assert (args.suite, args.iterations, args.cpu_baseline) == ("smoke", 100, False)
+    args = build_parser().parse_args(["compare", "transformer", "--seq", "7"])
+    assert (args.batch, args.seq, args.hidden, args.heads, args.intermediate) == (1, 7, 4096, 32, 11008)
+    args = build_parser().parse_args(["report", "--db", "x.db", "--out", "r"])
+    assert (args.db, args.out) == ("x.db", "r")
+
+
+def test_cli_commands_that_need_a_gpu_say_so():
+    for argv in (["benchmark", "vector_add", "--suite", "smoke", "--no-db"],
+                 ["compare", "rmsnorm", "--rows", "8", "--cols", "8"],
+                 ["compare", "transformer", "--seq", "1"]):
+        out = _cli(*argv)
+        assert out.returncode == 1 and "require a ROCm GPU" in out.stderr, argv
+
+
+def test_cli_report_without_a_database_exits_2(tmp_path):
+    out = _cli("report", "--db", str(tmp_path / "none.db"), "--out", str(tmp_path / "r"))
+    assert out.returncode == 2 and "no results database" in out.stderr
 
 
 # --- timing statistics -----------------------------------------------------------------

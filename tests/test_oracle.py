@@ -226,3 +226,94 @@ def test_eps_outside_the_root_is_caught_on_a_small_row():
     expect = torch.from_numpy(ops.rmsnorm_fp64(x, torch.ones(16), 1e-5))
     assert verify(expect, ops.rmsnorm_ref(x, torch.ones(16), 1e-5).double(), dtype=torch.float32).passed
     assert not verify(expect, _rmsnorm_eps_outside(x, torch.ones(16), 1e-5).double(), dtype=torch.float32).passed
+
+
+# --- vector_add: bit-exact against the IEEE definition -----------------------------
+
+_HALF = (torch.float16, torch.bfloat16)
+
+
+def _bits(t: torch.Tensor) -> torch.Tensor:
+    return t.contiguous().view(torch.int16)
+
+
+def _adversarial_pairs(dtype):
+    """Ties at every binade, sums that cancel, overflow to inf, subnormals."""
+    frac = {torch.float16: 10, torch.bfloat16: 7}[dtype]
+    half_ulp_of_one = 2.0 ** -(frac + 1)
+    a = [1.0, 1.0 + 2.0 ** -frac, 3.0, -1.0, 2.0 ** -14, 6.0e4, 1e-7, 0.0, -0.0]
+    b = [half_ulp_of_one, half_ulp_of_one, 3 * half_ulp_of_one * 2, -half_ulp_of_one,
+         2.0 ** -24, 6.0e4, -1e-7, -0.0, -0.0]
+    return torch.tensor(a).to(dtype), torch.tensor(b).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", _HALF, ids=["fp16", "bf16"])
+def test_vector_add_ref_is_the_correctly_rounded_sum(dtype):
+    g = torch.Generator().manual_seed(11)
+    scale = torch.exp(4 * torch.randn(4000, generator=g))
+    a = (torch.randn(4000, generator=g) * scale).to(dtype)
+    b = (torch.randn(4000, generator=g) * scale.flip(0)).to(dtype)
+    assert torch.equal(_bits(ops.vector_add_ref(a, b)), _bits(ops.vector_add_exact(a, b)))
+    a, b = _adversarial_pairs(dtype)
+    assert torch.equal(_bits(ops.vector_add_ref(a, b)), _bits(ops.vector_add_exact(a, b)))
+
+
+def test_exact_rounding_breaks_ties_to_even():
+    one = torch.tensor([1.0, 1.0 + 2.0 ** -10], dtype=torch.float16)
+    half_ulp = torch.full((2,), 2.0 ** -11, dtype=torch.float16)
+    out = ops.vector_add_exact(one, half_ulp).tolist()
+    assert out == [1.0, 1.0 + 2.0 ** -9]  # even neighbour each time
+    assert ops.vector_add_exact(torch.tensor([6.0e4], dtype=torch.float16),
+                                torch.tensor([6.0e4], dtype=torch.float16)).isinf().all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, *_HALF], ids=["fp32", "fp16", "bf16"])
+def test_vector_add_closed_forms(dtype):
+    g = torch.Generator().manual_seed(12)
+    a = torch.randn(1000, generator=g).to(dtype)
+    b = torch.randn(1000, generator=g).to(dtype)
+    assert torch.equal(ops.vector_add_ref(a, torch.zeros_like(a)), a)
+    neg = ops.vector_add_ref(a, -a)
+    assert (neg == 0).all() and not torch.signbit(neg).any()  # x + (-x) = +0 in round-to-nearest
+    assert torch.equal(ops.vector_add_ref(a, b), ops.vector_add_ref(b, a))
+
+
+def _truncating_add(a, b):
+    """Round toward zero instead of to nearest even: where rounding went up in
+    magnitude, step one unit of the 16-bit format back toward zero."""
+    s = a.double() + b.double()
+    q = s.to(a.dtype)
+    over = (q.double().abs() > s.abs()) & torch.isfinite(q)
+    toward_zero = (_bits(q) - 1).view(a.dtype)
+    return torch.where(over, toward_zero, q)
+
+
+def _double_rounded_add(a, b):
+    """fp16 sum rounded through bf16 first: too few bits in the intermediate."""
+    return (a.float() + b.float()).to(torch.bfloat16).to(a.dtype)
+
+
+@pytest.mark.parametrize("planted", [_truncating_add, _double_rounded_add,
+                                     lambda a, b: ops.vector_add_ref(a, -b)])
+def test_planted_vector_add_mistakes_fail_the_exact_check(planted):
+    g = torch.Generator().manual_seed(13)
+    a = torch.randn(2000, generator=g).to(torch.float16)
+    b = torch.randn(2000, generator=g).to(torch.float16)
+    assert not torch.equal(_bits(planted(a, b)), _bits(ops.vector_add_exact(a, b)))
+
+
+# --- the two-pass RMSNorm shares rmsnorm_ref: pin it at widths past 16384 ---------
+
+
+@pytest.mark.parametrize("cols", [16385, 40000])
+def test_rmsnorm_ref_matches_fp64_on_rows_past_the_single_pass_limit(cols):
+    g = torch.Generator().manual_seed(cols)
+    x = torch.randn(2, cols, generator=g)
+    gamma = 1 + 0.1 * torch.randn(cols, generator=g)
+    res = verify(torch.from_numpy(ops.rmsnorm_fp64(x, gamma, 1e-6)),
+                 ops.rmsnorm_ref(x, gamma, 1e-6).double(), dtype=torch.float32)
+    assert res.passed, res.reason
+    # Dividing by the single-pass block (16384) instead of the width must fail.
+    wrong = (x * torch.rsqrt(x.pow(2).sum(-1, keepdim=True) / 16384 + 1e-6) * gamma)
+    assert not verify(torch.from_numpy(ops.rmsnorm_fp64(x, gamma, 1e-6)), wrong.double(),
+                      dtype=torch.float32).passed

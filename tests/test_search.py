@@ -18,6 +18,9 @@ import torch
 from kernelo_amd.runtime.env import MI355X_CAPS
 from kernelo_amd.tuning.config import KernelConfig, Problem
 from kernelo_amd.tuning.search import (
+    TWO_PASS_MAX_STAGED_BYTES,
+    VectorAddSearchSpace,
+    two_pass_block,
     DEFAULT_MAX_CANDIDATES,
     MatmulSearchSpace,
     RMSNormSearchSpace,
@@ -219,7 +222,8 @@ def test_space_rejects_mismatched_problem():
     with pytest.raises(ValueError):
         MatmulSearchSpace().generate(Problem.create("softmax", "fp16", rows=2, cols=2), MI355X_CAPS)
     with pytest.raises(ValueError):
-        search_space("vector_add")
+        search_space("layernorm")
+    assert isinstance(search_space("vector_add"), VectorAddSearchSpace)
 
 
 def test_instantiation_list_is_the_rule_filtered_grid():
@@ -236,10 +240,21 @@ def test_instantiation_list_is_the_rule_filtered_grid():
 
 
 def test_row_space_shape():
-    problem = Problem.create("rmsnorm", "fp16", rows=4096, cols=4096)
-    result = RMSNormSearchSpace().generate(problem, MI355X_CAPS)
+    problem = Problem.create("softmax", "fp16", rows=4096, cols=4096)
+    result = SoftmaxSearchSpace().generate(problem, MI355X_CAPS)
     assert result.generated == 20
     assert all(c["BLOCK_SIZE"] == 4096 for c in result.candidates)
+    # RMSNorm adds the two-pass kernel as an algorithmic axis: 3 wave counts x
+    # 4 unrolls x 3 row counts x staged or not.
+    problem = Problem.create("rmsnorm", "fp16", rows=4096, cols=4096)
+    result = RMSNormSearchSpace().generate(problem, MI355X_CAPS)
+    assert result.generated == 20 + 72
+    single = [c for c in result.candidates if not c.get("TWO_PASS")]
+    assert single and all(c["BLOCK_SIZE"] == 4096 for c in single)
+    # Single-pass reads the row once from registers, so it ranks first.
+    assert not result.candidates[0].get("TWO_PASS")
+    first_two_pass = next(i for i, c in enumerate(result.candidates) if c.get("TWO_PASS"))
+    assert all(c.get("TWO_PASS") for c in result.candidates[first_two_pass:])
 
 
 def test_row_space_rules():
@@ -269,7 +284,66 @@ def test_default_row_config_is_feasible_up_to_the_limit(cols):
 def test_single_pass_limit_is_sixteen_thousand_values():
     assert RMSNormSearchSpace.MAX_BLOCK_SIZE == 16384
     p = Problem.create("rmsnorm", "fp32", rows=8, cols=16385)
-    assert all("single-pass limit" in r for _, r in RMSNormSearchSpace().generate(p, MI355X_CAPS).rejected)
+    result = RMSNormSearchSpace().generate(p, MI355X_CAPS)
+    single = [(c, r) for c, r in result.rejected if not c.get("TWO_PASS")]
+    assert len(single) == 20 and all("single-pass limit" in r for _, r in single)
+    # Past the limit only the two-pass kernel is left.
+    assert result.candidates and all(c["TWO_PASS"] == 1 for c in result.candidates)
+
+
+def test_two_pass_rules():
+    space = RMSNormSearchSpace()
+    reasons = lambda p: {r.split(":")[0] for _, r in space.generate(p, MI355X_CAPS).rejected}
+    wide32 = Problem.create("rmsnorm", "fp32", rows=4096, cols=65536)
+    got = reasons(wide32)
+    assert "register pressure" in got  # 8 vectors per lane at 16 waves
+    assert "LDS" in got                # 256 KiB rows cannot be staged
+    cands = space.candidates(wide32, MI355X_CAPS)
+    assert all(not c["STAGE_ROW"] for c in cands)
+    staged = space.candidates(Problem.create("rmsnorm", "fp16", rows=4096, cols=65536), MI355X_CAPS)
+    assert staged[0]["STAGE_ROW"] == 1  # 128 KiB of fp16 fits the 159 KiB budget
+    narrow = Problem.create("rmsnorm", "fp32", rows=4096, cols=1024)
+    assert "idle lanes" in reasons(narrow)
+    assert TWO_PASS_MAX_STAGED_BYTES == 159 * 1024
+    # The trip width is a whole number of 16-byte vectors per lane for every dtype.
+    for elem in (2, 4):
+        for w in (4, 8, 16):
+            for u in (1, 2, 4, 8):
+                assert two_pass_block(w, u, elem) % (w * 64 * (16 // elem)) == 0
+
+
+@pytest.mark.parametrize("cols", [16385, 32768, 40704, 40705, 1 << 20])
+@pytest.mark.parametrize("dtype", ["fp32", "fp16", "bf16"])
+def test_default_config_past_the_limit_is_a_feasible_two_pass_config(cols, dtype):
+    from kernelo_amd.dtypes import itemsize, parse_dtype
+
+    cfg = default_row_config("rmsnorm", cols, parse_dtype(dtype))
+    assert cfg["TWO_PASS"] == 1
+    assert cfg["STAGE_ROW"] == int(cols * itemsize(parse_dtype(dtype)) <= TWO_PASS_MAX_STAGED_BYTES)
+    problem = Problem.create("rmsnorm", dtype, rows=64, cols=cols)
+    assert RMSNormSearchSpace().reject_reason(cfg, problem, MI355X_CAPS) is None
+    # Softmax stays single-pass: its default past the limit is rejected by name.
+    soft = default_row_config("softmax", cols)
+    assert "single-pass limit" in SoftmaxSearchSpace().reject_reason(
+        soft, Problem.create("softmax", dtype, rows=64, cols=cols), MI355X_CAPS)
+
+
+def test_vector_add_space():
+    space = VectorAddSearchSpace()
+    big = Problem.create("vector_add", "fp32", n=1 << 26)
+    result = space.generate(big, MI355X_CAPS)
+    assert result.generated == 7 * 5
+    reasons = {r.split(":")[0] for _, r in result.rejected}
+    assert reasons == {"idle lanes", "register pressure"}
+    top = result.candidates[0]
+    lane_bytes = top["BLOCK_SIZE"] // (top["num_warps"] * 64) * 4
+    assert lane_bytes == 64 and space.num_programs(top, big) >= MI355X_CAPS.cu_count
+    # Every feasible config holds 1..64 elements per lane (the compiled set).
+    for c in result.candidates:
+        per_lane = c["BLOCK_SIZE"] // (c["num_warps"] * 64)
+        assert 1 <= per_lane <= 64 and per_lane & (per_lane - 1) == 0
+    tiny = space.candidates(Problem.create("vector_add", "fp16", n=1), MI355X_CAPS)
+    assert tiny  # nothing fills the GPU, so nothing is pruned
 
 
 def test_explain_names_the_device_and_every_stage():
