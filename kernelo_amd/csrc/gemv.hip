@@ -13,6 +13,12 @@
 // slices through an fp32 workspace -- the last workgroup to finish a strip
 // (atomic ticket) sums the slices in ascending order.
 //
+// W laid out k-contiguous (nn.Linear's weight, passed as weight.t(), so
+// ldw_k == 1) takes gemv_dot instead: LPR lanes split one column's k-run into
+// 16-byte vectors (a wave load covers 64/LPR columns), x is read the same
+// way, and the LPR partial sums of a column meet in a butterfly. Both
+// kernels end in the same cross-slice tail.
+//
 // The reference has no GEMV: decode runs through matmul_kernel with
 // BLOCK_M=16 (kernels/matmul.py:54-113, tuning/search.py:377-386).
 #include <math.h>
@@ -27,7 +33,6 @@ namespace {
 
 constexpr int kGemvMaxWaves = 16;
 constexpr size_t kGemvMaxLds = 64 * 1024;  // dynamic LDS without an opt-in attribute
-constexpr int kMinStripColumns = 32;       // LPR=8 lanes x 4 fp32 columns
 constexpr float kGeluC = 1.5957691216057308f;  // 2*sqrt(2/pi)
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -46,6 +51,98 @@ template <int MR>
 constexpr int gemv_max_lanes() { return MR == 4 ? 1024 : 512; }
 template <int MR>
 constexpr int gemv_unroll() { return MR <= 1 ? 16 : (MR <= 2 ? 8 : 4); }
+
+// The end both kernels share. red[(w*MR + m)*BN + c] holds red_waves partial
+// sums per (row m, column c of the block); each thread owns columns t,
+// t + nthreads, ... and combines the partials in ascending order. With split_k
+// slices, the slice publishes its sums to the fp32 workspace and the last
+// slice of the block to arrive (atomic ticket) adds them in slice order and
+// writes y; otherwise y is written directly. Callers synchronise the
+// workgroup after filling red.
+template <typename T, int MR>
+__device__ __forceinline__ void finish_block(const float* red, int red_waves, int BN, int64_t nb,
+                                             int64_t M, int64_t N, int s, int split_k,
+                                             int epilogue, const T* __restrict__ bias,
+                                             T* __restrict__ y, int64_t ldy_m, int64_t ldy_n,
+                                             float* __restrict__ ws,
+                                             unsigned* __restrict__ tickets) {
+  const int t = threadIdx.x;
+  const int nthreads = blockDim.x;
+  auto wave_sum = [&](int m, int c) {
+    float r = 0.f;
+    for (int w = 0; w < red_waves; ++w) r += red[(w * MR + m) * BN + c];
+    return r;
+  };
+  if (split_k > 1) {
+    // Publish this slice's partial sums, then take a ticket for the block.
+    // The partials move through agent-scope relaxed atomic stores/loads,
+    // which are coherent across XCDs without writing back or invalidating
+    // whole L2s (what a device-scope fence costs here); the only ordering
+    // needed is that every thread's stores have completed before the
+    // workgroup's ticket is taken.
+    for (int c = t; c < BN; c += nthreads) {
+      const int64_t col = nb * BN + c;
+      if (col >= N) continue;
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        if (m >= M) break;
+        __hip_atomic_store(ws + (static_cast<int64_t>(s) * M + m) * N + col, wave_sum(m, c),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial stores are done
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __shared__ unsigned ticket;
+    __syncthreads();  // every thread's stores are done
+    if (t == 0)
+      ticket = __hip_atomic_fetch_add(&tickets[nb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (ticket != static_cast<unsigned>(split_k - 1)) return;
+    // Sum the slices in ascending order (deterministic). kSliceBatch slices'
+    // loads are issued before any is added, so they are in flight together.
+    constexpr int kSliceBatch = 4;
+    for (int c = t; c < BN; c += nthreads) {
+      const int64_t col = nb * BN + c;
+      const int64_t cl = (col < N) ? col : N - 1;  // threads past N read a valid column
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        if (m >= M) break;
+        const float* src = ws + static_cast<int64_t>(m) * N + cl;
+        float r = 0.f;
+        for (int q0 = 0; q0 < split_k; q0 += kSliceBatch) {
+          float part[kSliceBatch];
+#pragma unroll
+          for (int b = 0; b < kSliceBatch; ++b) {
+            const int q = (q0 + b < split_k) ? q0 + b : split_k - 1;
+            part[b] = __hip_atomic_load(src + static_cast<int64_t>(q) * M * N, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+          }
+#pragma unroll
+          for (int b = 0; b < kSliceBatch; ++b)
+            if (q0 + b < split_k) r += part[b];
+        }
+        if (col >= N) continue;
+        if (epilogue == KF_EPILOGUE_BIAS_GELU) r = gelu_tanh(r + to_f32(bias[col]));
+        y[m * ldy_m + col * ldy_n] = from_f32<T>(r);
+      }
+    }
+    if (t == 0) __hip_atomic_store(&tickets[nb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+
+  for (int c = t; c < BN; c += nthreads) {
+    const int64_t col = nb * BN + c;
+    if (col >= N) continue;
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      if (m >= M) break;
+      float r = wave_sum(m, c);
+      if (epilogue == KF_EPILOGUE_BIAS_GELU) r = gelu_tanh(r + to_f32(bias[col]));
+      y[m * ldy_m + col * ldy_n] = from_f32<T>(r);
+    }
+  }
+}
 
 template <typename T, int MR, int LPR>
 __global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_splitk(
@@ -167,88 +264,104 @@ __global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_splitk(
   }
   __syncthreads();
 
-  // From here each thread owns columns t, t + nthreads, ... of the strip and
-  // combines the waves in ascending order.
-  const int t = threadIdx.x;
-  auto wave_sum = [&](int m, int c) {
-    float r = 0.f;
-    for (int w = 0; w < nwaves; ++w) r += red[(w * MR + m) * BN + c];
-    return r;
-  };
-  if (split_k > 1) {
-    // Publish this slice's partial sums, then take a ticket for the strip.
-    // The partials move through agent-scope relaxed atomic stores/loads,
-    // which are coherent across XCDs without writing back or invalidating
-    // whole L2s (what a device-scope fence costs here); the only ordering
-    // needed is that every thread's stores have completed before the
-    // workgroup's ticket is taken.
-    for (int c = t; c < BN; c += nthreads) {
-      const int64_t col = nb * BN + c;
-      if (col >= N) continue;
-#pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        if (m >= M) break;
-        __hip_atomic_store(ws + (static_cast<int64_t>(s) * M + m) * N + col, wave_sum(m, c),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial stores are done
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __shared__ unsigned ticket;
-    __syncthreads();  // every thread's stores are done
-    if (t == 0)
-      ticket = __hip_atomic_fetch_add(&tickets[nb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (ticket != static_cast<unsigned>(split_k - 1)) return;
-    // Sum the slices in ascending order (deterministic). kSliceBatch slices'
-    // loads are issued before any is added, so they are in flight together.
-    constexpr int kSliceBatch = 4;
-    for (int c = t; c < BN; c += nthreads) {
-      const int64_t col = nb * BN + c;
-      const int64_t cl = (col < N) ? col : N - 1;  // threads past N read a valid column
-#pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        if (m >= M) break;
-        const float* src = ws + static_cast<int64_t>(m) * N + cl;
-        float r = 0.f;
-        for (int q0 = 0; q0 < split_k; q0 += kSliceBatch) {
-          float part[kSliceBatch];
-#pragma unroll
-          for (int b = 0; b < kSliceBatch; ++b) {
-            const int q = (q0 + b < split_k) ? q0 + b : split_k - 1;
-            part[b] = __hip_atomic_load(src + static_cast<int64_t>(q) * M * N, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
-          }
-#pragma unroll
-          for (int b = 0; b < kSliceBatch; ++b)
-            if (q0 + b < split_k) r += part[b];
-        }
-        if (col >= N) continue;
-        if (epilogue == KF_EPILOGUE_BIAS_GELU) r = gelu_tanh(r + to_f32(bias[col]));
-        y[m * ldy_m + col * ldy_n] = from_f32<T>(r);
-      }
-    }
-    if (t == 0) __hip_atomic_store(&tickets[nb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
-  }
+  finish_block<T, MR>(red, nwaves, BN, nb, M, N, s, split_k, epilogue, bias, y, ldy_m, ldy_n, ws,
+                      tickets);
+}
 
-  for (int c = t; c < BN; c += nthreads) {
-    const int64_t col = nb * BN + c;
-    if (col >= N) continue;
+// k-contiguous W (ldw_k == 1, ldw_n = row pitch of nn.Linear's weight).
+// A wave load covers G = 64/LPR columns: lane l reads the 16-byte vector at
+// k = kbeg + (j*LPR + l%LPR)*V of column l/LPR, and the matching vector of
+// each x row, U vectors per lane in flight. The workgroup's waves take
+// adjacent column groups, so a block is nwaves*G columns of one K slice.
+template <int MR>
+constexpr int gemv_dot_unroll() { return MR <= 2 ? 8 : (MR <= 4 ? 4 : 2); }
+
+template <typename T, int MR, int LPR>
+__global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_dot(
+    const T* __restrict__ x, const T* __restrict__ W, const T* __restrict__ bias,
+    T* __restrict__ y, int64_t M, int64_t N, int64_t K, int64_t ldx_m, int64_t ldw_n,
+    int64_t ldy_m, int64_t ldy_n, int epilogue, int split_k, float* __restrict__ ws,
+    unsigned* __restrict__ tickets) {
+  constexpr int V = Vec<T>::N;
+  constexpr int G = kWave / LPR;  // columns per wave load
+  constexpr int U = gemv_dot_unroll<MR>();
+  extern __shared__ float red[];  // red[m][column of the block]
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int nwaves = blockDim.x / kWave;
+  const int BN = nwaves * G;
+  const int64_t nb = blockIdx.x;
+  const int cw = wave * G + lane / LPR;  // this lane's column within the block
+  const int64_t col = nb * BN + cw;
+  const int64_t col_ld = (col < N) ? col : N - 1;  // past N: a valid column, never stored
+  const int s = blockIdx.y;
+  // Slices are whole vectors so every load is one aligned 16-byte access.
+  const int64_t kc = ceil_div(ceil_div(K, split_k), V) * V;
+  const int64_t kbeg = static_cast<int64_t>(s) * kc;
+  const int64_t kend = (kbeg + kc < K) ? kbeg + kc : K;
+  constexpr int64_t kStep = static_cast<int64_t>(LPR) * V;  // k per wave load and column
+  const T* wcol = W + col_ld * ldw_n;
+
+  const T* xrow[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) xrow[m] = x + ((m < M) ? m : M - 1) * ldx_m;
+
+  float acc[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+  auto dot8 = [&](const u32x4 (&xr)[MR], const u32x4& wr) {
+    T w[V];
+    __builtin_memcpy(w, &wr, 16);
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-      if (m >= M) break;
-      float r = wave_sum(m, c);
-      if (epilogue == KF_EPILOGUE_BIAS_GELU) r = gelu_tanh(r + to_f32(bias[col]));
-      y[m * ldy_m + col * ldy_n] = from_f32<T>(r);
+      T xv[V];
+      __builtin_memcpy(xv, &xr[m], 16);
+#pragma unroll
+      for (int e = 0; e < V; ++e) acc[m] = __builtin_fmaf(to_f32(xv[e]), to_f32(w[e]), acc[m]);
     }
+  };
+
+  int64_t k = kbeg + (lane % LPR) * V;
+  for (; k + (U - 1) * kStep < kend; k += U * kStep) {
+    u32x4 wr[U];
+    u32x4 xr[U][MR];
+#pragma unroll
+    for (int u = 0; u < U; ++u) wr[u] = *reinterpret_cast<const u32x4*>(wcol + k + u * kStep);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        xr[u][m] = *reinterpret_cast<const u32x4*>(xrow[m] + k + u * kStep);
+    // All of the trip's loads issue before the first use.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) dot8(xr[u], wr[u]);
   }
+  for (; k < kend; k += kStep) {
+    u32x4 xr[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) xr[m] = *reinterpret_cast<const u32x4*>(xrow[m] + k);
+    dot8(xr, *reinterpret_cast<const u32x4*>(wcol + k));
+  }
+
+  // The LPR lanes of a column: butterfly over the low lane bits.
+#pragma unroll
+  for (int off = 1; off < LPR; off <<= 1)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] += __shfl_xor(acc[m], off, kWave);
+  if (lane % LPR == 0) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) red[m * BN + cw] = acc[m];
+  }
+  __syncthreads();
+  finish_block<T, MR>(red, 1, BN, nb, M, N, s, split_k, epilogue, bias, y, ldy_m, ldy_n, ws,
+                      tickets);
 }
 
 size_t ticket_bytes(int64_t N) {
-  // One ticket per strip; the narrowest strip has kMinStripColumns columns.
-  return static_cast<size_t>((ceil_div(N, kMinStripColumns) * 4 + 255) / 256 * 256);
+  // One ticket per column block; a gemv_dot block may be a single column.
+  return static_cast<size_t>((N * 4 + 255) / 256 * 256);
 }
 
 template <typename T>
@@ -258,8 +371,10 @@ int launch_gemv(const void* x, const void* W, const void* bias, void* y, int64_t
                 void* ws, hipStream_t s) {
   constexpr int V = Vec<T>::N;
   const bool vec = ldw_n == 1 && aligned16(W) && (ldw_k * sizeof(T)) % 16 == 0;
-  const dim3 grid(static_cast<unsigned>(ceil_div(N, static_cast<int64_t>(lpr) * V)),
-                  static_cast<unsigned>(split_k));
+  const int64_t es = static_cast<int64_t>(sizeof(T));
+  // k-contiguous W and x, 16-byte aligned rows, whole vectors of k.
+  const bool dot = ldw_k == 1 && ldx_k == 1 && K % V == 0 && aligned16(W) && aligned16(x) &&
+                   (ldw_n * es) % 16 == 0 && (M == 1 || (ldx_m * es) % 16 == 0);
   const dim3 block(waves * kWave);
   unsigned* tickets = static_cast<unsigned*>(ws);
   float* partial = ws ? reinterpret_cast<float*>(static_cast<char*>(ws) + ticket_bytes(N)) : nullptr;
@@ -271,6 +386,17 @@ int launch_gemv(const void* x, const void* W, const void* bias, void* y, int64_t
                 gemv_max_lanes<MR>() / kWave, waves);
       return KF_ERR_OUT_OF_RESOURCES;
     }
+    if (dot) {
+      const int64_t bn = static_cast<int64_t>(waves) * (kWave / LPR);
+      const dim3 grid(static_cast<unsigned>(ceil_div(N, bn)), static_cast<unsigned>(split_k));
+      const size_t lds = static_cast<size_t>(MR) * bn * sizeof(float);
+      hipLaunchKernelGGL((gemv_dot<T, MR, LPR>), grid, block, lds, s, static_cast<const T*>(x),
+                         static_cast<const T*>(W), static_cast<const T*>(bias), static_cast<T*>(y),
+                         M, N, K, ldx_m, ldw_n, ldy_m, ldy_n, epilogue, split_k, partial, tickets);
+      return launch_status("gemv");
+    }
+    const dim3 grid(static_cast<unsigned>(ceil_div(N, static_cast<int64_t>(lpr) * V)),
+                    static_cast<unsigned>(split_k));
     const size_t lds = static_cast<size_t>(waves) * MR * LPR * V * sizeof(float);
     if (lds > kGemvMaxLds) {
       set_error("gemv: waves=%d x %d rows needs %zu B of LDS for the wave reduction (limit %zu)",

@@ -46,6 +46,9 @@ def test_every_kernel_is_present(kernels):
     assert sum("softmax_rows" in n for n in kernels) == 3 * 7
     assert sum("rmsnorm_rows" in n for n in kernels) == 3 * 7
     assert sum("gemv_splitk" in n for n in kernels) == 3 * 4 * 4  # dtypes x row counts x strip widths
+    assert sum("gemv_dot" in n for n in kernels) == 3 * 4 * 4  # dtypes x row counts x lanes per column
+    assert sum("rmsnorm_two_pass" in n for n in kernels) == 3 * 4 * 2  # dtypes x unrolls x staging
+    assert sum("vector_add_kernel" in n for n in kernels) == 3 * 7  # dtypes x elements per lane
 
 
 def test_no_kernel_spills_to_scratch(kernels):

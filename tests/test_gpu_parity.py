@@ -327,6 +327,56 @@ def test_gemv_small_batches(m, dtype, lanes):
     _gate(ops.matmul_ref(x, w), out, dtype, f"gemv m={m}")
 
 
+# --- GEMV over nn.Linear weights: W k-contiguous (weight.t()) ---------------------
+
+
+@pytest.mark.parametrize("split", (1, 3, 8))
+@pytest.mark.parametrize("warps", (1, 4, 8))
+@pytest.mark.parametrize("lanes", (8, 16, 32, 64))
+def test_gemv_k_contiguous_weight(split, warps, lanes):
+    """x @ weight.t() with weight [N, K] row-major: the dot layout."""
+    from kernelo_amd.kernels.matmul import matmul
+
+    g = torch.Generator().manual_seed(1)
+    x = (torch.rand(1, 4096, generator=g) * 2 - 1).to(torch.bfloat16)
+    weight = (torch.rand(3001, 4096, generator=g) * 2 - 1).to(torch.bfloat16)
+    cfg = KernelConfig("matmul", GEMV=1, SPLIT_K=split, LANES_PER_ROW=lanes, num_warps=warps)
+    out = matmul(x.to(DEV), weight.to(DEV).t(), config=cfg)
+    _gate(ops.matmul_ref(x, weight.t()), out, torch.bfloat16, str(cfg))
+
+
+@pytest.mark.parametrize("m", (1, 2, 3, 5, 8))
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("k", (1000, 1004, 8, 0))
+def test_gemv_k_contiguous_batches_and_odd_k(m, dtype, k):
+    """Rows of x, every dtype; K % 8 != 0 (1004 fp16) takes the general path."""
+    from kernelo_amd.kernels.fused_linear import fused_linear_gelu
+    from kernelo_amd.kernels.matmul import matmul
+
+    x = _randn(m, k, dtype=dtype, seed=m + k)
+    weight = _randn(777, k, dtype=dtype, seed=3, scale=max(k, 1) ** -0.5)
+    bias = _randn(777, dtype=dtype, seed=4, scale=0.1)
+    cfg = KernelConfig("matmul", GEMV=1, SPLIT_K=2, LANES_PER_ROW=16, num_warps=4)
+    dx, dw = x.to(DEV), weight.to(DEV).t()
+    _gate(ops.matmul_ref(x, weight.t()), matmul(dx, dw, config=cfg), dtype, f"m={m} k={k}")
+    fcfg = KernelConfig("fused_linear", GEMV=1, SPLIT_K=2, LANES_PER_ROW=16, num_warps=4)
+    _gate(ops.linear_gelu_ref(x, weight.t(), bias),
+          fused_linear_gelu(dx, dw, bias.to(DEV), config=fcfg), dtype, f"fused m={m} k={k}")
+
+
+def test_gemv_k_contiguous_is_deterministic_and_matches_the_strip_kernel():
+    from kernelo_amd.kernels.matmul import matmul
+
+    x = _randn(1, 4096, dtype=torch.float16, seed=5).to(DEV)
+    weight = _randn(11008, 4096, dtype=torch.float16, seed=6, scale=1 / 64).to(DEV)
+    cfg = KernelConfig("matmul", GEMV=1, SPLIT_K=4, LANES_PER_ROW=16, num_warps=4)
+    first = matmul(x, weight.t(), config=cfg)
+    for _ in range(3):
+        assert torch.equal(matmul(x, weight.t(), config=cfg), first)
+    strip = matmul(x, weight.t().contiguous(), config=cfg)
+    assert verify(strip.cpu().double(), first.cpu(), dtype=torch.float16).passed
+
+
 # --- guard bands: bit-exact masks -------------------------------------------------
 
 
