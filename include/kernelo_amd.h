@@ -116,9 +116,13 @@ int kf_gemm_variant_info(int index, int* dtype, int* block_m, int* block_n, int*
  * (kernels/matmul.py:132-155, tuning/search.py:377-386); this is its
  * HBM-bound replacement. A workgroup of `waves` wavefronts owns a strip of
  * lanes_per_row (8, 16, 32 or 64) 16-byte vectors of columns and one of
- * `split_k` slices of K. Partial sums over the slices are reduced
- * deterministically (fixed order) by the last workgroup of each strip, using
- * a caller-provided workspace of kf_gemv_workspace_bytes() bytes whose
+ * `split_k` slices of K. When W is k-contiguous (ldw_k == 1, e.g.
+ * nn.Linear's weight passed as weight.t()) with x k-contiguous, 16-byte
+ * aligned rows and K a multiple of 16 bytes' worth of elements, the
+ * lanes_per_row lanes split one column's k-run instead, 64/lanes_per_row
+ * columns per wave load. Partial sums over the slices are reduced
+ * deterministically (fixed order) by the last workgroup of each column block,
+ * using a caller-provided workspace of kf_gemv_workspace_bytes() bytes whose
  * counter region must be zero before the first call (the kernel leaves it
  * zero again). epilogue as for kf_gemm.
  */
