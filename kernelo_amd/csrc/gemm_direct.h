@@ -25,7 +25,8 @@
 //     the 8 consecutive k a v_mfma_f32_16x16x32 lane needs.
 //   * The second 32-wide k step of each slice is multiplied after the
 //     barrier, while the next slice's first fragments are read, so every
-//     wave has MFMAs to issue during its own LDS latency.
+//     wave has MFMAs to issue during its own LDS latency; scheduling groups
+//     alternate LDS reads and MFMAs one for one.
 //
 // Requirements (checked on the host): 16-bit dtype, A k-contiguous with a
 // 16-byte aligned base and row pitch, B either n-contiguous (BLAYOUT 0) or
@@ -326,17 +327,42 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
       for (int j = 0; j < FN; ++j) Mma<T>::run(af[i], bf[j], acc[i][j]);
   };
   // Step 1 of each slice is carried over and multiplied after the barrier,
-  // while step 0 of the next slice loads (sched_barrier keeps the reads first).
+  // while step 0 of the next slice loads. The scheduling groups pin the
+  // order: LDS reads and MFMAs alternate one for one, so the reads of step 0
+  // run under the carried MFMAs and the reads of step 1 under step 0's, and
+  // by the barrier's lgkmcnt(0) only the last few reads are outstanding. Left
+  // to itself the scheduler issues step 1's reads late and waits for them at
+  // the barrier with most of step 0's MFMAs still to issue.
   u32x4 ca[FM], cb[FN];
   using First = std::integral_constant<bool, true>;
   using Next = std::integral_constant<bool, false>;
+  constexpr int kReads = FM + (BLAYOUT == 0 ? 2 : 1) * FN;  // LDS reads per k step
+  constexpr int kMfma = FM * FN;                           // MFMAs per k step
+  constexpr int kPairs = kReads < kMfma ? kReads : kMfma;
   auto compute = [&](const char* S, auto first) {
     u32x4 af[FM], bf[FN];
     load_frags(S, 0, af, bf);
-    __builtin_amdgcn_sched_barrier(0);
     if constexpr (!decltype(first)::value) mma_all(ca, cb);
     load_frags(S, 1, ca, cb);
     mma_all(af, bf);
+    if constexpr (decltype(first)::value) {
+      __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // step 0 reads
+    } else {
+#pragma unroll
+      for (int q = 0; q < kPairs; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      }
+      if constexpr (kMfma > kPairs) __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kPairs, 0);
+      if constexpr (kReads > kPairs) __builtin_amdgcn_sched_group_barrier(0x100, kReads - kPairs, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < kPairs; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+    if constexpr (kMfma > kPairs) __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kPairs, 0);
+    if constexpr (kReads > kPairs) __builtin_amdgcn_sched_group_barrier(0x100, kReads - kPairs, 0);
   };
 
   // ---- main loop ------------------------------------------------------------------
