@@ -23,10 +23,9 @@
 //     (row0 + i/4, col0 + 4*(i%4)) receives column col0+i of rows
 //     row0..row0+3, which is the MFMA B-operand layout. Two such reads give
 //     the 8 consecutive k a v_mfma_f32_16x16x32 lane needs.
-//   * The second 32-wide k step of each slice is multiplied after the
-//     barrier, while the next slice's first fragments are read, so every
-//     wave has MFMAs to issue during its own LDS latency; scheduling groups
-//     alternate LDS reads and MFMAs one for one.
+//   * Scheduling groups interleave the fragment reads of a slice's second
+//     32-wide k step with the MFMAs of its first, so LDS latency is spent
+//     under MFMAs and the reads are done by the slice's barrier.
 //
 // Requirements (checked on the host): 16-bit dtype, A k-contiguous with a
 // 16-byte aligned base and row pitch, B either n-contiguous (BLAYOUT 0) or
@@ -326,43 +325,33 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
 #pragma unroll
       for (int j = 0; j < FN; ++j) Mma<T>::run(af[i], bf[j], acc[i][j]);
   };
-  // Step 1 of each slice is carried over and multiplied after the barrier,
-  // while step 0 of the next slice loads. The scheduling groups pin the
-  // order: LDS reads and MFMAs alternate one for one, so the reads of step 0
-  // run under the carried MFMAs and the reads of step 1 under step 0's, and
-  // by the barrier's lgkmcnt(0) only the last few reads are outstanding. Left
-  // to itself the scheduler issues step 1's reads late and waits for them at
-  // the barrier with most of step 0's MFMAs still to issue.
-  u32x4 ca[FM], cb[FN];
-  using First = std::integral_constant<bool, true>;
-  using Next = std::integral_constant<bool, false>;
+  // Both 32-wide k steps of a slice are read and multiplied before its
+  // barrier. The scheduling groups pin the order: step 0's reads, then step
+  // 1's reads alternating one for one with step 0's MFMAs, then step 1's
+  // MFMAs, so each wave's reads run under its own (and the SIMD's other
+  // wave's) MFMAs and the barrier's lgkmcnt(0) finds them done. Left to
+  // itself the scheduler issues step 1's reads late and waits for them at
+  // the barrier with most MFMAs still to issue. (Carrying step 1's MFMAs
+  // over the barrier instead measured slower: it keeps a third fragment set
+  // live.)
   constexpr int kReads = FM + (BLAYOUT == 0 ? 2 : 1) * FN;  // LDS reads per k step
   constexpr int kMfma = FM * FN;                           // MFMAs per k step
   constexpr int kPairs = kReads < kMfma ? kReads : kMfma;
-  auto compute = [&](const char* S, auto first) {
-    u32x4 af[FM], bf[FN];
-    load_frags(S, 0, af, bf);
-    if constexpr (!decltype(first)::value) mma_all(ca, cb);
-    load_frags(S, 1, ca, cb);
-    mma_all(af, bf);
-    if constexpr (decltype(first)::value) {
-      __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // step 0 reads
-    } else {
-#pragma unroll
-      for (int q = 0; q < kPairs; ++q) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-      }
-      if constexpr (kMfma > kPairs) __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kPairs, 0);
-      if constexpr (kReads > kPairs) __builtin_amdgcn_sched_group_barrier(0x100, kReads - kPairs, 0);
-    }
+  auto compute = [&](const char* S) {
+    u32x4 a0[FM], b0[FN], a1[FM], b1[FN];
+    load_frags(S, 0, a0, b0);
+    load_frags(S, 1, a1, b1);
+    mma_all(a0, b0);
+    mma_all(a1, b1);
+    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // step 0 reads
 #pragma unroll
     for (int q = 0; q < kPairs; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one step-1 read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one step-0 MFMA
     }
     if constexpr (kMfma > kPairs) __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kPairs, 0);
     if constexpr (kReads > kPairs) __builtin_amdgcn_sched_group_barrier(0x100, kReads - kPairs, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, kMfma, 0);  // step 1 MFMAs
   };
 
   // ---- main loop ------------------------------------------------------------------
@@ -374,30 +363,30 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
       wait_vm<0>();
       fix(s0, 0);
       lds_barrier();
-      auto step = [&](char* cur, char* nxt, int64_t t, auto first) {
+      auto step = [&](char* cur, char* nxt, int64_t t) {
         if (t < nk) {
           if (t + 1 < nk) issue(nxt, t + 1);
-          compute(cur, first);
+          compute(cur);
           wait_vm<0>();
           if (t + 1 < nk) fix(nxt, t + 1);
           lds_barrier();
         }
       };
-      step(s0, s1, 0, First{});
+      step(s0, s1, 0);
       int64_t kt = 1;
       for (; kt + 3 <= nk; kt += 2) {  // slices kt (s1) and kt+1 (s0)
         issue(s0, kt + 1);             // kt+1 <= nk-2: never the partial slice
-        compute(s1, Next{});
+        compute(s1);
         wait_vm<0>();
         lds_barrier();
         issue(s1, kt + 2);             // kt+2 may be the partial last slice
-        compute(s0, Next{});
+        compute(s0);
         wait_vm<0>();
         fix(s1, kt + 2);
         lds_barrier();
       }
-      step(s1, s0, kt, Next{});
-      step(s0, s1, kt + 1, Next{});
+      step(s1, s0, kt);
+      step(s0, s1, kt + 1);
     } else {
       issue(s0, 0);
       if (nk > 1) {
@@ -408,10 +397,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
       }
       fix(s0, 0);
       lds_barrier();
-      auto step = [&](char* cur, char* nxt, char* pre, int64_t t, auto first) {
+      auto step = [&](char* cur, char* nxt, char* pre, int64_t t) {
         if (t < nk) {
           if (t + 2 < nk) issue(pre, t + 2);
-          compute(cur, first);
+          compute(cur);
           if (t + 2 < nk)
             wait_vm<kPer>();
           else
@@ -420,31 +409,30 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
           lds_barrier();
         }
       };
-      step(s0, s1, s2, 0, First{});
+      step(s0, s1, s2, 0);
       int64_t kt = 1;
       // Slices kt (s1), kt+1 (s2), kt+2 (s0). The slices waited for here
       // (kt+1..kt+3 <= nk-2) are never the partial one; kt+4 may be, and the
       // step that waits for it (t = kt+3, below or in the next trip) zeroes it.
       for (; kt + 5 <= nk; kt += 3) {
         issue(s0, kt + 2);
-        compute(s1, Next{});
+        compute(s1);
         wait_vm<kPer>();
         lds_barrier();
         issue(s1, kt + 3);
-        compute(s2, Next{});
+        compute(s2);
         wait_vm<kPer>();
         lds_barrier();
         issue(s2, kt + 4);
-        compute(s0, Next{});
+        compute(s0);
         wait_vm<kPer>();
         lds_barrier();
       }
-      step(s1, s2, s0, kt, Next{});
-      step(s2, s0, s1, kt + 1, Next{});
-      step(s0, s1, s2, kt + 2, Next{});
-      step(s1, s2, s0, kt + 3, Next{});
+      step(s1, s2, s0, kt);
+      step(s2, s0, s1, kt + 1);
+      step(s0, s1, s2, kt + 2);
+      step(s1, s2, s0, kt + 3);
     }
-    mma_all(ca, cb);  // step 1 of the last slice
   }
 
   // ---- epilogue -------------------------------------------------------------
