@@ -42,15 +42,15 @@ __device__ __forceinline__ float gelu_tanh(float a) {
   return a / (1.0f + __builtin_amdgcn_exp2f(-inner * kLog2e));
 }
 
-// Registers per lane: one x row keeps 16 rows of W (64 registers) in
-// flight, two keep 8, more keep 4, and all of a trip's loads are live at
-// once; eight x rows need 8x the accumulators and x values. Only four rows
-// fit 128 registers (a 1024-lane workgroup); the others cap it at 512 lanes
-// (256 registers each).
+// Registers per lane: trips are double buffered, so one x row keeps 2 x 8
+// rows of W (64 registers) in flight, two keep 2 x 4, more keep 2 x 2; eight
+// x rows need 8x the accumulators and x values. Only four rows fit 128
+// registers (a 1024-lane workgroup); the others cap it at 512 lanes (256
+// registers each).
 template <int MR>
 constexpr int gemv_max_lanes() { return MR == 4 ? 1024 : 512; }
 template <int MR>
-constexpr int gemv_unroll() { return MR <= 1 ? 16 : (MR <= 2 ? 8 : 4); }
+constexpr int gemv_unroll() { return MR <= 1 ? 8 : (MR <= 2 ? 4 : 2); }
 
 // The end both kernels share. red[(w*MR + m)*BN + c] holds red_waves partial
 // sums per (row m, column c of the block); each thread owns columns t,
@@ -201,21 +201,19 @@ __global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_splitk(
     const T* wcol = W + col_ld;
     // U rows per lane per trip. The x values go first so that the wait for
     // them does not also wait for the W rows behind them; then all W loads
-    // issue back to back and are consumed in order.
-    for (; k + (U - 1) * step < kend; k += U * step) {
-      T xt[U][MR];
+    // issue back to back and are consumed in order. Trips are double
+    // buffered: the next trip's loads are in flight while this one is
+    // multiplied, so a wave streams without a latency gap between trips.
+    auto load_trip = [&](int64_t kk, T (&xt)[U][MR], u32x4 (&raw)[U]) {
 #pragma unroll
       for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int m = 0; m < MR; ++m) xt[u][m] = xrow[m][(k + u * step) * ldx_k];
-      u32x4 raw[U];
+        for (int m = 0; m < MR; ++m) xt[u][m] = xrow[m][(kk + u * step) * ldx_k];
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        raw[u] = *reinterpret_cast<const u32x4*>(wcol + (k + u * step) * ldw_k);
-      // Every load of the trip is issued before any value is used: without
-      // this the scheduler converts each x right after its load and waits
-      // for it, serialising the trip's memory latencies.
-      __builtin_amdgcn_sched_barrier(0);
+        raw[u] = *reinterpret_cast<const u32x4*>(wcol + (kk + u * step) * ldw_k);
+    };
+    auto use_trip = [&](const T (&xt)[U][MR], const u32x4 (&raw)[U]) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         float xv[MR];
@@ -225,7 +223,30 @@ __global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_splitk(
         __builtin_memcpy(w, &raw[u], 16);
         fma_row(xv, w);
       }
+    };
+    const int64_t trip = U * step;
+    const int64_t span = kend - k - (U - 1) * step;  // trips t with k + t*trip + (U-1)*step < kend
+    const int64_t ntrips = span > 0 ? ceil_div(span, trip) : 0;
+    T xa[U][MR], xb[U][MR];
+    u32x4 ra[U], rb[U];
+    if (ntrips > 0) load_trip(k, xa, ra);
+    int64_t t = 0;
+    // The scheduling barriers keep each trip's loads ahead of the previous
+    // trip's multiplies: without them the scheduler converts each value right
+    // after its load and waits for it, serialising the memory latencies.
+    for (; t + 1 < ntrips; t += 2) {
+      load_trip(k + (t + 1) * trip, xb, rb);
+      __builtin_amdgcn_sched_barrier(0);
+      use_trip(xa, ra);
+      if (t + 2 < ntrips) load_trip(k + (t + 2) * trip, xa, ra);
+      __builtin_amdgcn_sched_barrier(0);
+      use_trip(xb, rb);
     }
+    if (t < ntrips) {
+      __builtin_amdgcn_sched_barrier(0);
+      use_trip(xa, ra);
+    }
+    k += ntrips * trip;
     for (; k < kend; k += step) {
       float xv[MR];
 #pragma unroll

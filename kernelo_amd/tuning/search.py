@@ -363,8 +363,9 @@ GEMV_DEFAULT_LANES_PER_ROW = 64
 
 
 def gemv_unroll(rows: int) -> int:
-    """Rows of W each lane keeps in flight per trip (gemv.hip gemv_unroll)."""
-    return 16 if rows <= 1 else (8 if rows <= 2 else 4)
+    """Rows of W each lane loads per trip (gemv.hip gemv_unroll); trips are
+    double buffered, so twice as many are in flight."""
+    return 8 if rows <= 1 else (4 if rows <= 2 else 2)
 
 
 class _GemmSpace(SearchSpace):
