@@ -23,6 +23,13 @@ constexpr int kMaxRowValues = 16384;
 template <int EPT>
 constexpr int max_lanes() { return (kMaxRowValues / EPT < 1024) ? kMaxRowValues / EPT : 1024; }
 constexpr float kLog2e = 1.4426950408889634f;
+// Rows of at most four 16-byte vectors per lane keep the next row's raw
+// loads in flight during the current row's reductions (16 extra registers
+// at most); wider rows already hold enough loads per lane.
+template <typename T, int EPT>
+constexpr bool prefetch_rows() {
+  return EPT >= 16 / static_cast<int>(sizeof(T)) && EPT * static_cast<int>(sizeof(T)) <= 64;
+}
 
 // Lane `t` of a `nt`-lane workgroup owns vector slots t, t+nt, t+2nt, ... of
 // the row; slot s covers columns [s*V, s*V+V). `vec` says whether the row is
@@ -76,6 +83,31 @@ struct RowTile {
 #pragma unroll
         for (int e = 0; e < V; ++e) v[j * V + e] = (c0 < cols) ? to_f32(tmp[e]) : fill;
       }
+    }
+  }
+
+  // The vector path split in two, so that the next row's loads can be in
+  // flight while this row is reduced: issue the raw 16-byte loads, convert
+  // later. Valid only where vector_ok() holds.
+  struct Raw {
+    u32x4 raw[NV];
+  };
+  __device__ __forceinline__ static void load_raw(Raw& r, const T* row, int64_t cols, int t,
+                                                  int nt) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t c0 = (static_cast<int64_t>(j) * nt + t) * V;
+      r.raw[j] = *reinterpret_cast<const u32x4*>(row + ((c0 < cols) ? c0 : cols - V));
+    }
+  }
+  __device__ __forceinline__ void convert(const Raw& r, int64_t cols, int t, int nt, float fill) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t c0 = (static_cast<int64_t>(j) * nt + t) * V;
+      T tmp[V];
+      __builtin_memcpy(tmp, &r.raw[j], 16);
+#pragma unroll
+      for (int e = 0; e < V; ++e) v[j * V + e] = (c0 < cols) ? to_f32(tmp[e]) : fill;
     }
   }
 
@@ -146,12 +178,8 @@ __global__ __launch_bounds__(max_lanes<EPT>()) void softmax_rows(const T* __rest
   const int t = threadIdx.x;
   const int nt = blockDim.x;
   const int nwaves = nt / kWave;
-  for (int i = 0; i < rpp; ++i) {
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * rpp + i;
-    if (r >= rows) break;
-    RowTile<T, EPT> tile;
-    // Out-of-row lanes hold -inf: they lose the max and add exp(-inf)=0.
-    tile.load(x + r * xrs, cols, t, nt, vec, -INFINITY);
+  using Tile = RowTile<T, EPT>;
+  auto process = [&](Tile& tile, int64_t r) {
     float m = -INFINITY;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) m = fmaxf(m, tile.v[e]);
@@ -167,6 +195,31 @@ __global__ __launch_bounds__(max_lanes<EPT>()) void softmax_rows(const T* __rest
     s = block_reduce<false>(s, part, slot, nwaves);
     const float inv = 1.0f / s;
     tile.store(y + r * yrs, cols, t, nt, vec, [inv](float v, int) { return v * inv; });
+  };
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rpp;
+  // Out-of-row lanes hold -inf: they lose the max and add exp(-inf)=0.
+  if constexpr (prefetch_rows<T, EPT>()) {
+    if (Tile::vector_ok(vec, cols)) {
+      typename Tile::Raw cur, nxt;
+      if (r0 < rows) Tile::load_raw(cur, x + r0 * xrs, cols, t, nt);
+      for (int i = 0; i < rpp; ++i) {
+        const int64_t r = r0 + i;
+        if (r >= rows) break;
+        if (i + 1 < rpp && r + 1 < rows) Tile::load_raw(nxt, x + (r + 1) * xrs, cols, t, nt);
+        Tile tile;
+        tile.convert(cur, cols, t, nt, -INFINITY);
+        process(tile, r);
+        cur = nxt;
+      }
+      return;
+    }
+  }
+  for (int i = 0; i < rpp; ++i) {
+    const int64_t r = r0 + i;
+    if (r >= rows) break;
+    Tile tile;
+    tile.load(x + r * xrs, cols, t, nt, vec, -INFINITY);
+    process(tile, r);
   }
 }
 
@@ -185,12 +238,8 @@ __global__ __launch_bounds__(max_lanes<EPT>()) void rmsnorm_rows(const T* __rest
   RowTile<T, EPT> g;
   g.load(gamma, cols, t, nt, vec, 0.f);
   const float inv_cols = 1.0f / static_cast<float>(cols);
-  for (int i = 0; i < rpp; ++i) {
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * rpp + i;
-    if (r >= rows) break;
-    RowTile<T, EPT> tile;
-    // Out-of-row lanes hold 0, which adds nothing to the sum of squares.
-    tile.load(x + r * xrs, cols, t, nt, vec, 0.f);
+  using Tile = RowTile<T, EPT>;
+  auto process = [&](Tile& tile, int64_t r) {
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) ss = __builtin_fmaf(tile.v[e], tile.v[e], ss);
@@ -198,6 +247,31 @@ __global__ __launch_bounds__(max_lanes<EPT>()) void rmsnorm_rows(const T* __rest
     const float inv_rms = rsqrtf(ss * inv_cols + eps);
     tile.store(y + r * yrs, cols, t, nt, vec,
                [inv_rms, &g](float v, int e) { return (v * inv_rms) * g.v[e]; });
+  };
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rpp;
+  // Out-of-row lanes hold 0, which adds nothing to the sum of squares.
+  if constexpr (prefetch_rows<T, EPT>()) {
+    if (Tile::vector_ok(vec, cols)) {
+      typename Tile::Raw cur, nxt;
+      if (r0 < rows) Tile::load_raw(cur, x + r0 * xrs, cols, t, nt);
+      for (int i = 0; i < rpp; ++i) {
+        const int64_t r = r0 + i;
+        if (r >= rows) break;
+        if (i + 1 < rpp && r + 1 < rows) Tile::load_raw(nxt, x + (r + 1) * xrs, cols, t, nt);
+        Tile tile;
+        tile.convert(cur, cols, t, nt, 0.f);
+        process(tile, r);
+        cur = nxt;
+      }
+      return;
+    }
+  }
+  for (int i = 0; i < rpp; ++i) {
+    const int64_t r = r0 + i;
+    if (r >= rows) break;
+    Tile tile;
+    tile.load(x + r * xrs, cols, t, nt, vec, 0.f);
+    process(tile, r);
   }
 }
 
