@@ -67,6 +67,20 @@ enum {
   KF_EPILOGUE_BIAS_GELU = 1  /* C = gelu_tanh(A @ B + bias), fused_linear.py:94-104 */
 };
 
+/*
+ * Split-K workspaces (kf_gemv, kf_gemm_split_k) are laid out the same way
+ * for every shape: KF_WORKSPACE_COUNTER_BYTES of 32-bit arrival counters,
+ * one per output block (at most KF_WORKSPACE_COUNTERS blocks), then the fp32
+ * partial sums. The counters must be zero before a workspace's first use and
+ * every completed call leaves them zero; because their region never moves,
+ * partial sums of one call can never land where a later call expects a zero
+ * counter, so one workspace can serve any sequence of calls on one stream.
+ */
+enum {
+  KF_WORKSPACE_COUNTERS = 1 << 18,
+  KF_WORKSPACE_COUNTER_BYTES = 4 << 18
+};
+
 /* Library identification: ABI version and the offload target it was built for. */
 int kf_abi_version(void);
 const char* kf_build_target(void);
@@ -100,6 +114,30 @@ int kf_gemm(int dtype, const void* A, const void* B, const void* bias, void* C,
             int block_m, int block_n, int block_k, int waves, int stages, int group_m,
             int pipeline, void* stream);
 
+/*
+ * kf_gemm with the K dimension split over `split_k` (1..64) programs per
+ * output tile, for shapes whose tile count leaves CUs idle (few rows, e.g.
+ * M = 16..128 of a prefill or batched decode). The reference has no split-K
+ * GEMM: it launches matmul_kernel (kernels/matmul.py:132-155) with one
+ * program per tile at every M, and this is that call with the K loop shared
+ * out. Runs on the direct pipeline (pipeline argument implied); a layout the
+ * direct pipeline cannot take runs unsplit on the register-staged fallback,
+ * as kf_gemm does. Each program adds its k-range in fp32 and publishes the
+ * partial tile to `workspace`; the last of a tile's programs to arrive sums
+ * the partials in ascending order, so results are deterministic. The
+ * workspace (kf_gemm_workspace_bytes, 16-byte aligned, laid out as described
+ * at KF_WORKSPACE_COUNTERS: one counter per tile) may be shared with kf_gemv;
+ * launches sharing a workspace must not overlap.
+ */
+int kf_gemm_split_k(int dtype, const void* A, const void* B, const void* bias, void* C,
+                    int64_t M, int64_t N, int64_t K,
+                    int64_t lda_m, int64_t lda_k, int64_t ldb_k, int64_t ldb_n,
+                    int64_t ldc_m, int64_t ldc_n, int epilogue,
+                    int block_m, int block_n, int block_k, int waves, int stages, int group_m,
+                    int split_k, void* workspace, size_t workspace_bytes, void* stream);
+/* Workspace bytes kf_gemm_split_k needs (0 when split_k <= 1). */
+size_t kf_gemm_workspace_bytes(int64_t M, int64_t N, int block_m, int block_n, int split_k);
+
 /* 1 if (dtype, tile config, pipeline) has an instantiation in this build, else 0. */
 int kf_gemm_has_variant(int dtype, int block_m, int block_n, int block_k, int waves, int stages,
                         int pipeline);
@@ -122,9 +160,9 @@ int kf_gemm_variant_info(int index, int* dtype, int* block_m, int* block_n, int*
  * lanes_per_row lanes split one column's k-run instead, 64/lanes_per_row
  * columns per wave load. Partial sums over the slices are reduced
  * deterministically (fixed order) by the last workgroup of each column block,
- * using a caller-provided workspace of kf_gemv_workspace_bytes() bytes whose
- * counter region must be zero before the first call (the kernel leaves it
- * zero again). epilogue as for kf_gemm.
+ * using a caller-provided workspace of kf_gemv_workspace_bytes() bytes laid
+ * out as described at KF_WORKSPACE_COUNTERS (one counter per column block).
+ * epilogue as for kf_gemm.
  */
 int kf_gemv(int dtype, const void* x, const void* W, const void* bias, void* y,
             int64_t M, int64_t N, int64_t K,

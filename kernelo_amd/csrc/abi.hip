@@ -29,7 +29,7 @@ int launch_status(const char* what) {
 
 }  // namespace kf
 
-extern "C" int kf_abi_version(void) { return 3; }
+extern "C" int kf_abi_version(void) { return 4; }
 
 extern "C" const char* kf_build_target(void) { return "gfx950"; }
 

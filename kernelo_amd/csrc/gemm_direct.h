@@ -34,6 +34,16 @@
 // rows of B) below 4 GiB. BK is 64: one A row of a k-slice is 128 bytes.
 // M/N edges clamp rows/columns (results discarded); the partial last k-slice
 // clamps k into range and zeroes its chunks past K after the DMA lands.
+//
+// Split-K: with args.split_k = S > 1 the grid holds S programs per output
+// tile. Program s multiplies k-slices [s*P, (s+1)*P) (P = ceil(slices / S);
+// a trailing range may be short or empty) by moving its operand bases to
+// slice s*P and running the ordinary loop over a K of its own. It publishes
+// its fp32 accumulators to its partial tile in the workspace, in fragment
+// order (lane-contiguous, so the stores coalesce); the last of the S
+// programs to take the tile's ticket adds the S partials in ascending s --
+// the same order whichever program is last, so results are deterministic --
+// applies the epilogue, writes C and returns the ticket to zero.
 #pragma once
 
 #include <type_traits>
@@ -90,6 +100,17 @@ template <int N>
 __device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
   __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// Split-K partial tiles move through raw buffer stores and loads of 16 bytes
+// with the cache policy of the compiler's agent-scope atomic dword store/load
+// (sc1): coherent across XCDs without writing back or invalidating whole
+// L2s. The buffer resource covers one partial tile (bytes in num_records;
+// the third dword selects 32-bit data, as raw buffer access on gfx9 needs).
+constexpr int kBufferWord3 = 0x00020000;
+constexpr int kCachePolicySc1 = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(float* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(p, 0, bytes, kBufferWord3);
 }
 
 // Workgroup barrier for the DMA pipeline: this wave's LDS reads and writes
@@ -153,14 +174,27 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   char* const s1 = lds + Tl::kStageBytes;
   char* const s2 = lds + (STAGES == 3 ? 2 * Tl::kStageBytes : 0);
 
-  const int64_t M = args.M, N = args.N, K = args.K;
+  const int64_t M = args.M, N = args.N;
 
   // ---- tile order: regroup per XCD, then GROUP_M bands (as gemm_kernel) ----
+  // With split-K the regrouping runs over all S*tiles programs with s the
+  // slowest index, so one XCD's programs share a k-range and its rows of A.
   const int64_t tiles_m = ceil_div(M, BM);
   const int64_t tiles_n = ceil_div(N, BN);
   const int64_t ntiles = tiles_m * tiles_n;
+  const int split = args.split_k;
+  const int64_t nprog = ntiles * split;
   int64_t pid = blockIdx.x;
-  if (ntiles % kNumXcd == 0) pid = (pid % kNumXcd) * (ntiles / kNumXcd) + pid / kNumXcd;
+  if (nprog % kNumXcd == 0) pid = (pid % kNumXcd) * (nprog / kNumXcd) + pid / kNumXcd;
+  const int s_idx = split > 1 ? static_cast<int>(pid / ntiles) : 0;
+  if (split > 1) pid %= ntiles;
+  const int64_t tile = pid;
+  // This program's k-range: slices [kt0, kt0 + P), as a K of its own.
+  const int64_t slices_per = ceil_div(ceil_div(args.K, BK), static_cast<int64_t>(split));
+  const int64_t kt0 = s_idx * slices_per;
+  int64_t K = args.K - kt0 * BK;
+  K = K < slices_per * BK ? K : slices_per * BK;
+  K = K > 0 ? K : 0;
   const int64_t gm = args.group_m;
   const int64_t in_group = gm * tiles_n;
   const int64_t group = pid / in_group;
@@ -179,10 +213,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   // Chunk q = j*NT + tid is written to LDS slot q; its source is the chunk at
   // the slot's position XOR the row's swizzle. Rows past M (and columns or
   // rows of B past N) are clamped to the last valid one.
-  const char* const a_tile = static_cast<const char*>(args.A) + m0 * args.lda_m * 2;
+  const char* const a_tile = static_cast<const char*>(args.A) + m0 * args.lda_m * 2 + kt0 * BK * 2;
   const int64_t lda_b = args.lda_m * 2;
   const int64_t ldb_b = (BLAYOUT == 0 ? args.ldb_k : args.ldb_n) * 2;  // bytes per B row
-  const char* const b_tile = static_cast<const char*>(args.B) + (BLAYOUT == 0 ? n0 * 2 : n0 * ldb_b);
+  const char* const b_tile = static_cast<const char*>(args.B) +
+                             (BLAYOUT == 0 ? n0 * 2 + kt0 * BK * ldb_b : n0 * ldb_b + kt0 * BK * 2);
   constexpr int kRowsPerIter = NT / 8;  // k-contiguous rows (A, BLAYOUT 1) per DMA instruction
   const int kr = tid >> 3;              // this lane's row within an instruction's rows
   const int kc = swz_k(tid & 7, kr) * 8;  // its k within the slice; same for every j
@@ -433,6 +468,58 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
       step(s0, s1, s2, kt + 2);
       step(s1, s2, s0, kt + 3);
     }
+  }
+
+  // ---- split-K: publish the partial tile; the last program sums them -------
+  if (split > 1) {
+    // Partials move through agent-scope (sc1) stores and loads, which are
+    // coherent across XCDs without writing back or invalidating whole L2s;
+    // the only ordering needed is that every lane's stores have completed
+    // (vmcnt(0), then the workgroup barrier) before the ticket is taken.
+    // Fragment (i, j) of lane tid is the 16 bytes at ((i*FN + j)*NT + tid)*16.
+    constexpr int kTileFloats = BM * BN;
+    auto part = [&](int q) {
+      return tile_rsrc(args.ws + (static_cast<int64_t>(q) * ntiles + tile) * kTileFloats,
+                       kTileFloats * 4);
+    };
+    const __amdgpu_buffer_rsrc_t mine = part(s_idx);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), mine,
+                                               ((i * FN + j) * NT + tid) * 16, 0, kCachePolicySc1);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    wait_vm<0>();  // this lane's partial stores are done
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    // The K loop ended on a barrier, so the stage buffers are free: the
+    // ticket is broadcast through the first word of LDS.
+    unsigned* const ticket = reinterpret_cast<unsigned*>(lds);
+    __syncthreads();
+    if (tid == 0)
+      *ticket = __hip_atomic_fetch_add(&args.tickets[tile], 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (*ticket != static_cast<unsigned>(split - 1)) return;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < split; ++q) {
+      const __amdgpu_buffer_rsrc_t src = part(q);
+      u32x4 p[FM][FN];  // all of slice q's loads in flight before the first add
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          p[i][j] = __builtin_amdgcn_raw_buffer_load_b128(src, ((i * FN + j) * NT + tid) * 16, 0,
+                                                          kCachePolicySc1);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] += __builtin_bit_cast(f32x4, p[i][j]);
+    }
+    if (tid == 0) __hip_atomic_store(&args.tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   // ---- epilogue -------------------------------------------------------------

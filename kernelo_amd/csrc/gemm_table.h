@@ -16,6 +16,13 @@ struct Args {
   int64_t lda_m, lda_k, ldb_k, ldb_n, ldc_m, ldc_n;
   int epilogue;
   int group_m;
+  // Split-K (DMA pipeline only): split_k programs per output tile each take
+  // a contiguous range of k-slices; ws holds their fp32 partial tiles and
+  // tickets one counter per tile (zero between launches). split_k == 1 leaves
+  // both unused.
+  int split_k;
+  float* ws;
+  unsigned* tickets;
 };
 
 struct Entry {

@@ -380,10 +380,6 @@ __global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_dot(
                       tickets);
 }
 
-size_t ticket_bytes(int64_t N) {
-  // One ticket per column block; a gemv_dot block may be a single column.
-  return static_cast<size_t>((N * 4 + 255) / 256 * 256);
-}
 
 template <typename T>
 int launch_gemv(const void* x, const void* W, const void* bias, void* y, int64_t M, int64_t N,
@@ -398,7 +394,8 @@ int launch_gemv(const void* x, const void* W, const void* bias, void* y, int64_t
                    (ldw_n * es) % 16 == 0 && (M == 1 || (ldx_m * es) % 16 == 0);
   const dim3 block(waves * kWave);
   unsigned* tickets = static_cast<unsigned*>(ws);
-  float* partial = ws ? reinterpret_cast<float*>(static_cast<char*>(ws) + ticket_bytes(N)) : nullptr;
+  float* partial = ws ? reinterpret_cast<float*>(static_cast<char*>(ws) + KF_WORKSPACE_COUNTER_BYTES)
+                      : nullptr;
   auto go = [&](auto mr, auto lanes) -> int {
     constexpr int MR = decltype(mr)::value;
     constexpr int LPR = decltype(lanes)::value;
@@ -449,7 +446,8 @@ int launch_gemv(const void* x, const void* W, const void* bias, void* y, int64_t
 
 extern "C" size_t kf_gemv_workspace_bytes(int64_t M, int64_t N, int split_k) {
   if (M <= 0 || N <= 0 || split_k <= 1) return 0;
-  return kf::ticket_bytes(N) + static_cast<size_t>(split_k) * M * N * sizeof(float);
+  return static_cast<size_t>(KF_WORKSPACE_COUNTER_BYTES) +
+         static_cast<size_t>(split_k) * M * N * sizeof(float);
 }
 
 extern "C" int kf_gemv(int dtype, const void* x, const void* W, const void* bias, void* y,
@@ -492,6 +490,12 @@ extern "C" int kf_gemv(int dtype, const void* x, const void* W, const void* bias
     return KF_ERR_INVALID_ARGUMENT;
   }
   if (split_k > 1) {
+    // One counter per column block, and a block holds at least one column.
+    if (N > KF_WORKSPACE_COUNTERS) {
+      set_error("gemv: split_k=%d needs one counter per column block; N=%lld exceeds the %d "
+                "counters of a workspace", split_k, (long long)N, KF_WORKSPACE_COUNTERS);
+      return KF_ERR_INVALID_ARGUMENT;
+    }
     const size_t need = kf_gemv_workspace_bytes(M, N, split_k);
     if (!workspace || workspace_bytes < need || !aligned16(workspace)) {
       set_error("gemv: split_k=%d needs a 16-byte aligned workspace of %zu bytes, got %zu",

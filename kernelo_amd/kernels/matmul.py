@@ -4,8 +4,10 @@ Python surface of the reference's ``matmul`` (kernelforge/kernels/matmul.py:
 118-259): same signature, same validation messages (``_check_operands``,
 :123-129), output allocated with ``torch.empty`` in the input dtype, any
 operand strides accepted. The device work is one call into
-``libkernelo_amd.so``: ``kf_gemm`` (MFMA tiles) or, when the config carries
-``GEMV=1``, ``kf_gemv`` (split-K, HBM-bound, M <= 8).
+``libkernelo_amd.so``: ``kf_gemm`` (MFMA tiles), ``kf_gemm_split_k`` (the
+same tiles with K shared out over ``SPLIT_K`` programs per tile, for row
+counts whose tiles leave CUs idle) or, when the config carries ``GEMV=1``,
+``kf_gemv`` (split-K, HBM-bound, M <= 8).
 """
 
 from __future__ import annotations
@@ -82,6 +84,21 @@ def launch_gemm(
             stream,
         )
         hip.check(rc, "gemv")
+        return out
+    split = cfg.get("SPLIT_K", 1)
+    if split > 1:
+        need = lib.kf_gemm_workspace_bytes(m, n, cfg["BLOCK_M"], cfg["BLOCK_N"], split)
+        ws = hip.workspaces.get(a.device, stream, need) if need else None
+        rc = lib.kf_gemm_split_k(
+            code, a.data_ptr(), b.data_ptr(), bias_ptr, out.data_ptr(),
+            m, n, k, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
+            out.stride(0), out.stride(1), epilogue,
+            cfg["BLOCK_M"], cfg["BLOCK_N"], cfg["BLOCK_K"], cfg["num_warps"],
+            cfg.get("num_stages", 2), cfg.get("GROUP_M", 8), split,
+            ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+            stream,
+        )
+        hip.check(rc, "gemm")
         return out
     rc = lib.kf_gemm(
         code, a.data_ptr(), b.data_ptr(), bias_ptr, out.data_ptr(),

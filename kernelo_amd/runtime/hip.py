@@ -112,6 +112,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _int, _int, _int, _vp, _sz, _vp],
     ),
     "kf_gemv_workspace_bytes": (_sz, [_i64, _i64, _int]),
+    "kf_gemm_split_k": (
+        _int,
+        [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int,
+         _int, _int, _int, _int, _int, _int, _int, _vp, _sz, _vp],
+    ),
+    "kf_gemm_workspace_bytes": (_sz, [_i64, _i64, _int, _int, _int]),
     "kf_softmax": (_int, [_int, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _int, _vp]),
     "kf_rmsnorm": (
         _int,
@@ -205,8 +211,11 @@ def gemm_variants() -> list[tuple[int, int, int, int, int, int, int]]:
 class _Workspaces:
     """Per (device, stream) split-K workspace, zeroed when (re)allocated.
 
-    The GEMV's ticket counters must start at zero; the kernel returns them to
-    zero, so a buffer only needs clearing when it is first made.
+    Every split-K entry point (GEMV and GEMM) lays a workspace out the same
+    way: a fixed region of arrival counters, then fp32 partial sums. The
+    counters must start at zero and each completed call returns them to zero;
+    since their region is the same for every shape, one buffer serves any
+    sequence of calls on its stream and only needs clearing when it is made.
     """
 
     def __init__(self) -> None:

@@ -24,6 +24,8 @@ is unit-testable on a CPU-only host.
 
 from __future__ import annotations
 
+import math
+
 from abc import ABC, abstractmethod
 from collections.abc import Iterator
 from itertools import product
@@ -271,8 +273,8 @@ def gemm_tile_regs(
     """Per-lane register model of one tile: accumulators, fragments, staged loads.
 
     The direct pipeline stages nothing in registers (the DMA writes LDS) but
-    holds two k steps of fragments: one carried across the barrier while the
-    next slice's first step loads.
+    holds two k steps of fragments: the second step's are read while the
+    first step's MFMAs run.
     """
     lanes = waves * 64
     wm, wn = wave_grid(waves, block_m, block_n)
@@ -391,6 +393,13 @@ class _GemmSpace(SearchSpace):
     GEMV_LANES_PER_ROW = (8, 16, 32, 64)
     #: Dynamic LDS the GEMV wave reduction may use (gemv.hip kGemvMaxLds).
     GEMV_MAX_LDS = 64 * 1024
+    #: Split-K for DMA tiles: programs per output tile, offered while the
+    #: unsplit tiles leave CUs idle (few rows: prefill of short prompts,
+    #: batched decode).
+    TILE_SPLIT_K = (2, 4, 8, 16)
+    #: Fewest k-slices (of 64) a split program may own: below this the
+    #: pipeline's fill and the partial-tile traffic dominate.
+    TILE_SPLIT_MIN_SLICES = 4
 
     def grid(self, problem: Problem) -> Iterator[KernelConfig]:
         for direct, bm, bn, bk, warps, stages in product(
@@ -406,6 +415,20 @@ class _GemmSpace(SearchSpace):
                 num_warps=warps,
                 num_stages=stages,
             )
+        for bm, bn, warps, stages, split in product(
+            self.BLOCK_M, self.BLOCK_N, self.NUM_WARPS, self.NUM_STAGES, self.TILE_SPLIT_K
+        ):
+            yield KernelConfig(
+                self.operation,
+                BLOCK_M=bm,
+                BLOCK_N=bn,
+                BLOCK_K=64,
+                GROUP_M=self.GROUP_M,
+                DIRECT=1,
+                SPLIT_K=split,
+                num_warps=warps,
+                num_stages=stages,
+            )
         if problem.dims_dict["M"] <= self.GEMV_MAX_M:
             for split, lanes, warps in product(self.SPLIT_K, self.GEMV_LANES_PER_ROW, self.GEMV_WARPS):
                 yield KernelConfig(
@@ -418,7 +441,8 @@ class _GemmSpace(SearchSpace):
             lanes = config.get("LANES_PER_ROW", GEMV_DEFAULT_LANES_PER_ROW)
             strip = lanes * (VECTOR_BYTES // problem.itemsize)
             return ceil_div(dims["N"], strip) * config["SPLIT_K"]
-        return ceil_div(dims["M"], config["BLOCK_M"]) * ceil_div(dims["N"], config["BLOCK_N"])
+        tiles = ceil_div(dims["M"], config["BLOCK_M"]) * ceil_div(dims["N"], config["BLOCK_N"])
+        return tiles * config.get("SPLIT_K", 1)
 
     def reject_reason(self, config: KernelConfig, problem: Problem, caps: DeviceCaps) -> str | None:
         dims = problem.dims_dict
@@ -447,6 +471,28 @@ class _GemmSpace(SearchSpace):
             return f"tile overshoot: BLOCK_M={bm} for M={m}"
         if bn > 2 * n and bn > min(self.BLOCK_N):
             return f"tile overshoot: BLOCK_N={bn} for N={n}"
+        split = config.get("SPLIT_K", 1)
+        if split > 1:
+            if not config.get("DIRECT"):
+                return "split-K tiles: only the DMA pipeline splits K"
+            tiles = ceil_div(m, bm) * ceil_div(n, bn)
+            if tiles >= caps.cu_count:
+                return f"split-K tiles: {tiles} tiles already fill {caps.cu_count} CUs"
+            resident = gemm_resident_workgroups(config, caps)
+            if tiles * split > caps.cu_count * resident:
+                # Measured: a second round of split programs costs more than
+                # the split saves (512x11008x4096: 256x128 at 65 us unsplit,
+                # 87 us at SPLIT_K=2, 108 us at 4).
+                return (
+                    f"split-K tiles: {tiles * split} workgroups exceed one round of "
+                    f"{caps.cu_count} CUs x {resident} resident"
+                )
+            slices = ceil_div(ceil_div(k, 64), split)
+            if slices < self.TILE_SPLIT_MIN_SLICES:
+                return (
+                    f"split-K slice too short: {slices} k-slices per program at SPLIT_K={split} "
+                    f"(fewest {self.TILE_SPLIT_MIN_SLICES})"
+                )
         return None
 
     def _gemv_reason(self, config: KernelConfig, m: int, k: int, elem: int) -> str | None:
@@ -473,12 +519,14 @@ class _GemmSpace(SearchSpace):
     ) -> tuple[float, ...]:
         """Rank survivors for the budget.
 
-        GEMM tiles: (1) workgroups, saturating at one per CU, so that a large
-        problem ties and a small one prefers filling the GPU; (2) reuse
-        ``BM*BN/(BM+BN)`` -- the MFMA work per byte staged through LDS;
-        (3) least padding waste; then the DMA pipeline, more stages in
-        flight, and its 8-wave form (two waves per SIMD hide LDS latency);
-        register-staged tiles prefer fewer waves (more registers each).
+        GEMM tiles: (1) the DMA pipeline, which measured ahead of the
+        register-staged one at every fp16/bf16 shape tried; (2) the time
+        :func:`gemm_time_estimate` gives; (3) fewer split-K programs per
+        tile; (4) more stages in flight; (5) waves: 8 for DMA tiles of at
+        least 128x128, or 64x64 when split (two waves per SIMD hide LDS
+        latency), else 4, and fewer for register-staged tiles (more registers
+        each); (6) the taller of two
+        transposed tiles; (7) least padding waste.
         GEMV: HBM-bound, so (1) at least one workgroup per CU, (2) at least
         four waves per CU (each keeps 16 x 16 bytes per lane in flight, and
         HBM needs ~32 KiB in flight per CU), then fewer slices (a shorter
@@ -499,20 +547,92 @@ class _GemmSpace(SearchSpace):
                 config["num_warps"],
             )
         bm, bn = config["BLOCK_M"], config["BLOCK_N"]
-        reuse = (bm * bn) / (bm + bn)
+        direct = config.get("DIRECT", 0)
+        split = config.get("SPLIT_K", 1)
+        estimate = gemm_time_estimate(config, problem, caps)
         padded = ceil_div(dims["M"], bm) * bm * ceil_div(dims["N"], bn) * bn
         waste = padded / (dims["M"] * dims["N"])
+        if direct:
+            wide = bm * bn >= 128 * 128 or (split > 1 and bm * bn >= 64 * 64)
+            wave_rank = abs(config["num_warps"] - (8 if wide else 4))
+        else:
+            wave_rank = config["num_warps"]
         return (
             1,
-            -min(programs, caps.cu_count),
-            -reuse,
-            waste,
-            -config.get("DIRECT", 0),
+            -direct,
+            round(estimate * 1e6, 2),
+            split,
             -config["num_stages"],
-            # The DMA pipeline hides LDS latency with two waves per SIMD; the
-            # register-staged one prefers fewer, larger-register waves.
-            -config["num_warps"] if config.get("DIRECT") else config["num_warps"],
+            wave_rank,
+            bm < bn,
+            waste,
         )
+
+
+#: Reuse ``BM*BN/(BM+BN)`` of the 256x128 tile, the largest the DMA pipeline
+#: instantiates; the GEMM estimate treats it as the full MFMA rate.
+_FULL_RATE_REUSE = 256 * 128 / (256 + 128)
+#: Start-up and wind-down of one program's K loop, in k-slices of work: what
+#: makes splitting K into short ranges cost more than it saves.
+_PIPELINE_FILL_SLICES = 3
+#: MI355X rates the estimate is calibrated on (fp16, cache flushed): the
+#: 256x128 DMA tile sustains about 1.0 PFLOP/s over 256 CUs; streaming
+#: kernels reach about 5 TB/s of HBM; a program whose slices are latency-bound
+#: (few rows) advances about one 64-wide k-slice per 0.35 us.
+_CU_FLOPS = 1.0e15 / 256
+_HBM_BYTES_PER_S = 5.0e12
+_SLICE_LATENCY_S = 0.35e-6
+#: Waves one CU holds (8 per SIMD), for co-resident workgroups.
+_WAVES_PER_CU = 32
+
+
+def gemm_resident_workgroups(config: KernelConfig, caps: DeviceCaps, elem: int = 2) -> int:
+    """Workgroups of one MFMA-tile config a CU holds at once (LDS and waves)."""
+    bm, bn = config["BLOCK_M"], config["BLOCK_N"]
+    stages = config.get("num_stages", 2)
+    if config.get("DIRECT"):
+        lds = gemm_direct_lds_bytes(bm, bn, stages)
+    else:
+        lds = gemm_lds_bytes(bm, bn, config["BLOCK_K"], stages, elem)
+    return max(1, min(caps.lds_per_cu // max(lds, 1), _WAVES_PER_CU // config["num_warps"]))
+
+
+def gemm_time_estimate(config: KernelConfig, problem: Problem, caps: DeviceCaps) -> float:
+    """Seconds one MFMA-tile GEMM launch should take, from three bounds.
+
+    * compute: each CU runs ``ceil(workgroups / CUs)`` tiles back to back,
+      each ``BM*BN*64*2`` FLOP per k-slice (plus the pipeline's fill) at the
+      rate its reuse ``BM*BN/(BM+BN)`` sustains, ``sqrt(reuse / reuse_256x128)``
+      of the full rate;
+    * memory: the operands once, C once, and with split-K every program's
+      fp32 partial tile written and read back, at streaming HBM rate;
+    * latency: few-row tiles wait on each k-slice's DMA; co-resident
+      workgroups (as LDS and waves allow) wait together.
+
+    Calibrated on MI355X measurements: it ranks the one-pass 256x128 tile
+    first on large problems, 64x64/64x128 at M=512 and split-K 32x64/64x128
+    tiles that make one pass over the CUs at M=16..128.
+    """
+    dims = problem.dims_dict
+    m, n, k = dims["M"], dims["N"], dims["K"]
+    bm, bn, bk = config["BLOCK_M"], config["BLOCK_N"], config["BLOCK_K"]
+    split = config.get("SPLIT_K", 1)
+    elem = itemsize(problem.dtype)
+    tiles = ceil_div(m, bm) * ceil_div(n, bn)
+    programs = tiles * split
+    slices = ceil_div(ceil_div(k, bk), split) + _PIPELINE_FILL_SLICES
+    reuse = min((bm * bn) / (bm + bn), _FULL_RATE_REUSE)
+    rate = _CU_FLOPS * math.sqrt(reuse / _FULL_RATE_REUSE)
+    compute = ceil_div(programs, caps.cu_count) * bm * bn * bk * 2 * slices / rate
+    moved = (m * k + k * n + m * n) * elem
+    if split > 1:
+        moved += 2 * programs * bm * bn * 4
+    memory = moved / _HBM_BYTES_PER_S
+    resident = gemm_resident_workgroups(config, caps, elem)
+    latency = ceil_div(programs, caps.cu_count * resident) * slices * _SLICE_LATENCY_S
+    # A 4-norm rather than the plain maximum: the largest bound decides, and a
+    # config with slack in the other two ranks ahead of one without.
+    return (compute**4 + memory**4 + latency**4) ** 0.25
 
 
 class MatmulSearchSpace(_GemmSpace):

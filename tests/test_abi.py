@@ -37,6 +37,7 @@ def test_header_declares_the_expected_entry_points():
     assert _declared() == {
         "kf_abi_version", "kf_build_target", "kf_last_error",
         "kf_gemm", "kf_gemm_has_variant", "kf_gemm_variant_count", "kf_gemm_variant_info",
+        "kf_gemm_split_k", "kf_gemm_workspace_bytes",
         "kf_gemv", "kf_gemv_workspace_bytes", "kf_softmax", "kf_rmsnorm",
         "kf_rmsnorm_two_pass", "kf_rmsnorm_two_pass_max_staged_cols", "kf_vector_add",
     }
@@ -50,7 +51,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_identification(lib):
-    assert lib.kf_abi_version() == 3
+    assert lib.kf_abi_version() == 4
     assert lib.kf_build_target() == b"gfx950"
 
 
@@ -72,9 +73,15 @@ def test_variant_table_equals_the_instantiation_rules(lib):
 
 def test_workspace_sizing(lib):
     assert lib.kf_gemv_workspace_bytes(1, 11008, 1) == 0
-    tickets = (11008 * 4 + 255) // 256 * 256  # one per column block; a block may be one column
-    assert lib.kf_gemv_workspace_bytes(1, 11008, 8) == tickets + 8 * 11008 * 4
+    # Every split-K workspace: a fixed 1 MiB counter region, then fp32 partials.
+    counters = 1 << 20
+    assert lib.kf_gemv_workspace_bytes(1, 11008, 8) == counters + 8 * 11008 * 4
     assert lib.kf_gemv_workspace_bytes(0, 11008, 8) == 0
+    tiles = 1 * (11008 // 64)
+    assert lib.kf_gemm_workspace_bytes(32, 11008, 32, 64, 4) == counters + 4 * tiles * 32 * 64 * 4
+    assert lib.kf_gemm_workspace_bytes(30, 11000, 32, 64, 4) == counters + 4 * tiles * 32 * 64 * 4
+    assert lib.kf_gemm_workspace_bytes(32, 11008, 32, 64, 1) == 0
+    assert lib.kf_gemm_workspace_bytes(0, 11008, 32, 64, 4) == 0
 
 
 def _rc_and_message(rc_fn):
@@ -109,6 +116,32 @@ def test_gemm_argument_errors(lib):
     assert gemm(m=0) == hip.KF_OK and gemm(n=0) == hip.KF_OK
 
 
+def test_gemm_split_k_argument_errors(lib):
+    def gemm(split=4, ws=NULL, wsb=0, m=64, n=64, k=256, dtype=1, bm=64, bn=64):
+        return lib.kf_gemm_split_k(dtype, 1 << 20, 1 << 20, NULL, 1 << 20, m, n, k, k, 1, n, 1, n,
+                                   1, 0, bm, bn, 64, 4, 3, 8, split, ws, wsb, NULL)
+
+    need = lib.kf_gemm_workspace_bytes(64, 64, 64, 64, 4)
+    rc, msg = _rc_and_message(lambda: gemm(split=0))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "split_k" in msg
+    rc, msg = _rc_and_message(lambda: gemm(split=65))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "split_k" in msg
+    rc, msg = _rc_and_message(lambda: gemm())
+    assert rc == hip.KF_ERR_WORKSPACE and "workspace" in msg
+    rc, msg = _rc_and_message(lambda: gemm(ws=1 << 20, wsb=need - 4))
+    assert rc == hip.KF_ERR_WORKSPACE and str(need) in msg
+    rc, msg = _rc_and_message(lambda: gemm(ws=(1 << 20) + 4, wsb=need))
+    assert rc == hip.KF_ERR_WORKSPACE and "aligned" in msg
+    # One counter per tile: more tiles than the counter region holds is refused.
+    rc, msg = _rc_and_message(lambda: gemm(m=1 << 16, n=1 << 16, bm=64, bn=64))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "counters" in msg
+    rc, msg = _rc_and_message(lambda: gemm(dtype=0))  # fp32 has no direct pipeline
+    assert rc == hip.KF_ERR_NOT_BUILT and "direct" in msg
+    # split_k is only meaningful on the direct pipeline: kf_gemm never splits,
+    # and zero-size problems return before the workspace is looked at.
+    assert gemm(m=0) == hip.KF_OK and gemm(n=0) == hip.KF_OK
+
+
 def test_gemv_argument_errors(lib):
     def gemv(m=1, n=64, k=64, split=1, waves=4, ws=NULL, wsb=0, dtype=2, epi=0, lanes=16):
         return lib.kf_gemv(dtype, 1 << 20, 1 << 20, NULL, 1 << 20, m, n, k, k, 1, n, 1, n, 1, epi,
@@ -124,6 +157,8 @@ def test_gemv_argument_errors(lib):
     assert rc == hip.KF_ERR_INVALID_ARGUMENT and "split_k" in msg
     rc, msg = _rc_and_message(lambda: gemv(split=4))
     assert rc == hip.KF_ERR_WORKSPACE and "workspace" in msg
+    rc, msg = _rc_and_message(lambda: gemv(split=4, n=(1 << 18) + 8))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "counters" in msg
     rc, msg = _rc_and_message(lambda: gemv(dtype=4))
     assert rc == hip.KF_ERR_UNSUPPORTED_DTYPE
     rc, msg = _rc_and_message(lambda: gemv(epi=1))

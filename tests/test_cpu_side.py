@@ -175,7 +175,7 @@ def _cli(*args: str) -> subprocess.CompletedProcess:
 def test_cli_explain_and_env_work_without_a_gpu():
     out = _cli("tune", "matmul", "--m", "2048", "--n", "4096", "--k", "4096", "--explain")
     assert out.returncode == 0, out.stderr
-    assert "grid points      : 384" in out.stdout and "no device attached" in out.stdout
+    assert "grid points      : 640" in out.stdout and "no device attached" in out.stdout
     out = _cli("env")
     assert out.returncode == 0 and "Device limits" in out.stdout and "gfx950" in out.stdout
 

@@ -139,7 +139,11 @@ def test_direct_rules():
 
 def test_flagship_gemm_space_on_mi355x():
     result = MatmulSearchSpace().generate(_gemm(), MI355X_CAPS)
-    assert result.generated == 4 * 4 * 3 * 2 * 2 * 2  # BM x BN x BK x waves x stages x pipeline
+    # BM x BN x BK x waves x stages x pipeline, then the split-K DMA tiles:
+    # BM x BN x waves x stages x SPLIT_K (2, 4, 8, 16).
+    assert result.generated == 4 * 4 * 3 * 2 * 2 * 2 + 4 * 4 * 2 * 2 * 4
+    # 256 tiles of 256x128 already fill the CUs: no split survives.
+    assert not any(c.get("SPLIT_K", 1) > 1 for c in result.candidates)
     assert len(result.candidates) == DEFAULT_MAX_CANDIDATES
     # Every rejection is attributed to a named rule.
     assert all(":" in reason for _, reason in result.rejected)
@@ -216,6 +220,51 @@ def test_small_problems_prefer_parallelism():
     cands = MatmulSearchSpace().candidates(_gemm(256, 256, 256), MI355X_CAPS)
     first = cands[0]
     assert first["BLOCK_M"] * first["BLOCK_N"] <= 64 * 64
+
+
+@pytest.mark.parametrize(
+    "m, n, k, tile, split, warps",
+    [
+        # Fastest of about 100 measured candidates on MI355X (fp16, cache flushed).
+        (16, 4096, 4096, (32, 64), 4, 4),
+        (32, 11008, 4096, (32, 128), 2, 4),
+        (32, 4096, 11008, (32, 128), 8, 4),
+        (64, 11008, 4096, (64, 128), 2, 8),
+        (128, 11008, 4096, (128, 128), 2, 8),
+        (256, 4096, 11008, (128, 128), 4, 8),
+        (512, 11008, 4096, (256, 128), 1, 8),
+        (2048, 4096, 4096, (256, 128), 1, 8),
+        (2048, 11008, 4096, (256, 128), 1, 8),
+    ],
+)
+def test_top_gemm_candidate_matches_the_measured_winner(m, n, k, tile, split, warps):
+    first = MatmulSearchSpace().candidates(_gemm(m, n, k), MI355X_CAPS, max_candidates=1)[0]
+    assert (first["BLOCK_M"], first["BLOCK_N"]) == tile
+    assert first.get("SPLIT_K", 1) == split
+    assert first["DIRECT"] == 1 and first["num_stages"] == 3 and first["num_warps"] == warps
+
+
+def test_split_k_tiles_are_offered_only_while_tiles_leave_cus_idle():
+    space = MatmulSearchSpace(max_candidates=10_000)
+    skinny = space.generate(_gemm(32, 4096, 4096), MI355X_CAPS)
+    assert any(c.get("SPLIT_K", 1) > 1 for c in skinny.candidates)
+    assert "split-K tiles" in {r.split(":")[0] for _, r in skinny.rejected}
+    short = space.generate(_gemm(32, 4096, 512), MI355X_CAPS)  # 8 k-slices
+    assert "split-K slice too short" in {r.split(":")[0] for _, r in short.rejected}
+    assert all(c.get("SPLIT_K", 1) <= 2 for c in short.candidates)
+    for c in skinny.candidates:
+        split = c.get("SPLIT_K", 1)
+        if split > 1:
+            assert c["DIRECT"] == 1 and space.num_programs(c, _gemm(32, 4096, 4096)) <= 256 * 8
+            assert 64 // split >= MatmulSearchSpace.TILE_SPLIT_MIN_SLICES
+    # 256x128 at M=512 makes 172 tiles; a second round of split programs was
+    # measured slower (65 us unsplit, 87 us at SPLIT_K=2), so none is offered.
+    wide = space.generate(_gemm(512, 11008, 4096), MI355X_CAPS)
+    assert not any(c.get("SPLIT_K", 1) > 1 and c["BLOCK_M"] == 256 and c["BLOCK_N"] == 128
+                   for c in wide.candidates)
+    stale = KernelConfig("matmul", BLOCK_M=64, BLOCK_N=64, BLOCK_K=64, GROUP_M=8, DIRECT=0,
+                         SPLIT_K=4, num_warps=4, num_stages=2)
+    assert "DMA" in space.reject_reason(stale, _gemm(32, 4096, 4096), MI355X_CAPS)
 
 
 def test_space_rejects_mismatched_problem():
