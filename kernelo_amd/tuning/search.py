@@ -382,7 +382,8 @@ class _GemmSpace(SearchSpace):
     NUM_STAGES = (2, 3)
     #: 0: register-staged LDS pipeline; 1: global->LDS DMA pipeline.
     DIRECT = (0, 1)
-    GROUP_M = 8
+    #: Rows of tiles per launch-order band: derived from the tile by
+    #: :func:`gemm_group_m` rather than searched (it changes traffic, not time).
 
     #: Split-K GEMV grid, offered when M is at most GEMV_MAX_M.
     GEMV_MAX_M = 8
@@ -410,7 +411,7 @@ class _GemmSpace(SearchSpace):
                 BLOCK_M=bm,
                 BLOCK_N=bn,
                 BLOCK_K=bk,
-                GROUP_M=self.GROUP_M,
+                GROUP_M=gemm_group_m(bm, bn),
                 DIRECT=direct,
                 num_warps=warps,
                 num_stages=stages,
@@ -423,7 +424,7 @@ class _GemmSpace(SearchSpace):
                 BLOCK_M=bm,
                 BLOCK_N=bn,
                 BLOCK_K=64,
-                GROUP_M=self.GROUP_M,
+                GROUP_M=gemm_group_m(bm, bn),
                 DIRECT=1,
                 SPLIT_K=split,
                 num_warps=warps,
@@ -584,6 +585,29 @@ _HBM_BYTES_PER_S = 5.0e12
 _SLICE_LATENCY_S = 0.35e-6
 #: Waves one CU holds (8 per SIMD), for co-resident workgroups.
 _WAVES_PER_CU = 32
+
+
+#: CUs per XCD on MI355X: the workgroups one XCD's L2 serves at a time.
+_CUS_PER_XCD = 32
+
+
+def gemm_group_m(block_m: int, block_n: int) -> int:
+    """Band height (GROUP_M) that makes each XCD's concurrent tiles a near-square block.
+
+    Workgroups are dispatched to the 8 XCDs round-robin and the kernels regroup
+    them so that each XCD takes a contiguous run of tile indices; within a
+    band of GROUP_M tile rows consecutive indices walk down the band. One
+    XCD's 32 concurrent tiles then cover GROUP_M rows of A tiles and
+    32/GROUP_M columns of B tiles, and its L2 fetches
+    ``GROUP_M*BM + (32/GROUP_M)*BN`` rows of K per k-slice, least at
+    ``GROUP_M = sqrt(32*BN/BM)`` (rounded to a power of two). Measured on
+    MI355X: the 256x128 tile at 2048x4096x4096 runs in the same time at
+    GROUP_M 2..16 and fetches 160 MiB from beyond L2 at GROUP_M=8 (each XCD
+    reads all of A) but 128 MiB at 4; the fused 4096x11008x4096 launch fetches
+    1004 MiB at 8 and 729 MiB at 4.
+    """
+    ideal = math.sqrt(_CUS_PER_XCD * block_n / block_m)
+    return int(min(16, max(1, 2 ** math.floor(math.log2(ideal) + 0.5))))
 
 
 def gemm_resident_workgroups(config: KernelConfig, caps: DeviceCaps, elem: int = 2) -> int:
