@@ -116,8 +116,12 @@ int kf_gemm(int dtype, const void* A, const void* B, const void* bias, void* C,
 
 /*
  * kf_gemm with the K dimension split over `split_k` (1..64) programs per
- * output tile, for shapes whose tile count leaves CUs idle (few rows, e.g.
- * M = 16..128 of a prefill or batched decode). The reference has no split-K
+ * output tile, for shapes whose tile count leaves CUs idle: few rows (e.g.
+ * M = 16..128 of a prefill or batched decode), or a last round of tiles that
+ * fills only part of the GPU. When there are at least as many tiles as
+ * workgroups the device runs at once (kf_gemm_concurrent_tiles), only the
+ * tiles of the last, partial round are split (none when every round is
+ * full). The reference has no split-K
  * GEMM: it launches matmul_kernel (kernels/matmul.py:132-155) with one
  * program per tile at every M, and this is that call with the K loop shared
  * out. Runs on the direct pipeline (pipeline argument implied); a layout the
@@ -135,6 +139,12 @@ int kf_gemm_split_k(int dtype, const void* A, const void* B, const void* bias, v
                     int64_t ldc_m, int64_t ldc_n, int epilogue,
                     int block_m, int block_n, int block_k, int waves, int stages, int group_m,
                     int split_k, void* workspace, size_t workspace_bytes, void* stream);
+/* Workgroups of one GEMM variant the current device runs at once (CUs x the
+ * workgroups a CU holds by LDS, wave slots and registers): one round, the
+ * size that decides which tiles kf_gemm_split_k splits. A negative KF_ERR_*
+ * code on failure. No counterpart in the reference (Triton sizes nothing). */
+int64_t kf_gemm_concurrent_tiles(int dtype, int block_m, int block_n, int block_k, int waves,
+                                 int stages, int pipeline);
 /* Workspace bytes kf_gemm_split_k needs (0 when split_k <= 1). */
 size_t kf_gemm_workspace_bytes(int64_t M, int64_t N, int block_m, int block_n, int split_k);
 

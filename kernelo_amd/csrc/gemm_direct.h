@@ -36,7 +36,9 @@
 // clamps k into range and zeroes its chunks past K after the DMA lands.
 //
 // Split-K: with args.split_k = S > 1 the grid holds S programs per output
-// tile. Program s multiplies k-slices [s*P, (s+1)*P) (P = ceil(slices / S);
+// tile for the tiles from args.full_tiles on (all tiles when it is 0; the
+// tiles before it run one program each, so a launch can split only the
+// tiles of its last, partial round). Program s multiplies k-slices [s*P, (s+1)*P) (P = ceil(slices / S);
 // a trailing range may be short or empty) by moving its operand bases to
 // slice s*P and running the ordinary loop over a K of its own. It publishes
 // its fp32 accumulators to its partial tile in the workspace, in fragment
@@ -177,17 +179,28 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   const int64_t M = args.M, N = args.N;
 
   // ---- tile order: regroup per XCD, then GROUP_M bands (as gemm_kernel) ----
-  // With split-K the regrouping runs over all S*tiles programs with s the
-  // slowest index, so one XCD's programs share a k-range and its rows of A.
+  // Tiles [0, full) run one program each; the tiles after them (all tiles
+  // when full is 0) run args.split_k programs each. Each group's programs
+  // are regrouped per XCD on their own, the split ones with s the slowest
+  // index, so one XCD's programs share a k-range and its rows of A.
   const int64_t tiles_m = ceil_div(M, BM);
   const int64_t tiles_n = ceil_div(N, BN);
   const int64_t ntiles = tiles_m * tiles_n;
-  const int split = args.split_k;
-  const int64_t nprog = ntiles * split;
+  const int64_t full = args.split_k > 1 ? args.full_tiles : ntiles;
+  const int64_t split_tiles = ntiles - full;
   int64_t pid = blockIdx.x;
-  if (nprog % kNumXcd == 0) pid = (pid % kNumXcd) * (nprog / kNumXcd) + pid / kNumXcd;
-  const int s_idx = split > 1 ? static_cast<int>(pid / ntiles) : 0;
-  if (split > 1) pid %= ntiles;
+  int split = 1;
+  int s_idx = 0;
+  if (pid < full) {
+    if (full % kNumXcd == 0) pid = (pid % kNumXcd) * (full / kNumXcd) + pid / kNumXcd;
+  } else {
+    split = args.split_k;
+    const int64_t nsplit = split_tiles * split;
+    int64_t q = pid - full;
+    if (nsplit % kNumXcd == 0) q = (q % kNumXcd) * (nsplit / kNumXcd) + q / kNumXcd;
+    s_idx = static_cast<int>(q / split_tiles);
+    pid = full + q % split_tiles;
+  }
   const int64_t tile = pid;
   // This program's k-range: slices [kt0, kt0 + P), as a K of its own.
   const int64_t slices_per = ceil_div(ceil_div(args.K, BK), static_cast<int64_t>(split));
@@ -478,8 +491,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
     // (vmcnt(0), then the workgroup barrier) before the ticket is taken.
     // Fragment (i, j) of lane tid is the 16 bytes at ((i*FN + j)*NT + tid)*16.
     constexpr int kTileFloats = BM * BN;
+    const int64_t st = tile - full;  // index among the split tiles
     auto part = [&](int q) {
-      return tile_rsrc(args.ws + (static_cast<int64_t>(q) * ntiles + tile) * kTileFloats,
+      return tile_rsrc(args.ws + (static_cast<int64_t>(q) * split_tiles + st) * kTileFloats,
                        kTileFloats * 4);
     };
     const __amdgpu_buffer_rsrc_t mine = part(s_idx);
@@ -497,7 +511,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
     unsigned* const ticket = reinterpret_cast<unsigned*>(lds);
     __syncthreads();
     if (tid == 0)
-      *ticket = __hip_atomic_fetch_add(&args.tickets[tile], 1u, __ATOMIC_RELAXED,
+      *ticket = __hip_atomic_fetch_add(&args.tickets[st], 1u, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (*ticket != static_cast<unsigned>(split - 1)) return;
@@ -519,7 +533,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] += __builtin_bit_cast(f32x4, p[i][j]);
     }
-    if (tid == 0) __hip_atomic_store(&args.tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(&args.tickets[st], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   // ---- epilogue -------------------------------------------------------------

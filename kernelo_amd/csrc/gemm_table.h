@@ -16,11 +16,12 @@ struct Args {
   int64_t lda_m, lda_k, ldb_k, ldb_n, ldc_m, ldc_n;
   int epilogue;
   int group_m;
-  // Split-K (DMA pipeline only): split_k programs per output tile each take
-  // a contiguous range of k-slices; ws holds their fp32 partial tiles and
-  // tickets one counter per tile (zero between launches). split_k == 1 leaves
-  // both unused.
+  // Split-K (DMA pipeline only): tiles [full_tiles, tiles) run split_k
+  // programs each, every one over a contiguous range of k-slices; ws holds
+  // their fp32 partial tiles and tickets one counter per split tile (zero
+  // between launches). split_k == 1 leaves full_tiles, ws and tickets unused.
   int split_k;
+  int64_t full_tiles;
   float* ws;
   unsigned* tickets;
 };

@@ -118,6 +118,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _int, _int, _int, _int, _int, _int, _int, _vp, _sz, _vp],
     ),
     "kf_gemm_workspace_bytes": (_sz, [_i64, _i64, _int, _int, _int]),
+    "kf_gemm_concurrent_tiles": (_i64, [_int, _int, _int, _int, _int, _int, _int]),
     "kf_softmax": (_int, [_int, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _int, _vp]),
     "kf_rmsnorm": (
         _int,

@@ -477,16 +477,20 @@ class _GemmSpace(SearchSpace):
             if not config.get("DIRECT"):
                 return "split-K tiles: only the DMA pipeline splits K"
             tiles = ceil_div(m, bm) * ceil_div(n, bn)
-            if tiles >= caps.cu_count:
-                return f"split-K tiles: {tiles} tiles already fill {caps.cu_count} CUs"
-            resident = gemm_resident_workgroups(config, caps)
-            if tiles * split > caps.cu_count * resident:
+            round_ = caps.cu_count * gemm_resident_workgroups(config, caps)
+            # Only the tiles of the last, partial round are split (all of them
+            # when there is a single round); the kernel runs the rest unsplit.
+            tail = tiles % round_ if tiles >= round_ else tiles
+            if tail == 0:
+                return f"split-K tiles: {tiles} tiles fill whole rounds of {round_} workgroups"
+            if tail * split > round_:
                 # Measured: a second round of split programs costs more than
                 # the split saves (512x11008x4096: 256x128 at 65 us unsplit,
-                # 87 us at SPLIT_K=2, 108 us at 4).
+                # 87 us at SPLIT_K=2, 108 us at 4; 2048x11008x4096: 197 us
+                # unsplit, 215 us when its 176-tile last round is split in two).
                 return (
-                    f"split-K tiles: {tiles * split} workgroups exceed one round of "
-                    f"{caps.cu_count} CUs x {resident} resident"
+                    f"split-K tiles: {tail} split tiles x {split} exceed one round of "
+                    f"{round_} workgroups"
                 )
             slices = ceil_div(ceil_div(k, 64), split)
             if slices < self.TILE_SPLIT_MIN_SLICES:
@@ -627,15 +631,18 @@ def gemm_time_estimate(config: KernelConfig, problem: Problem, caps: DeviceCaps)
     * compute: each CU runs ``ceil(workgroups / CUs)`` tiles back to back,
       each ``BM*BN*64*2`` FLOP per k-slice (plus the pipeline's fill) at the
       rate its reuse ``BM*BN/(BM+BN)`` sustains, ``sqrt(reuse / reuse_256x128)``
-      of the full rate;
+      of the full rate; with several rounds of tiles only the last, partial
+      round is split, so its programs are shorter;
     * memory: the operands once, C once, and with split-K every program's
       fp32 partial tile written and read back, at streaming HBM rate;
     * latency: few-row tiles wait on each k-slice's DMA; co-resident
       workgroups (as LDS and waves allow) wait together.
 
-    Calibrated on MI355X measurements: it ranks the one-pass 256x128 tile
-    first on large problems, 64x64/64x128 at M=512 and split-K 32x64/64x128
-    tiles that make one pass over the CUs at M=16..128.
+    Calibrated on MI355X measurements: over the 50 tuned fp16 shapes from
+    M=16 to 4096 its first candidate measures 4% above the tuned winner on
+    average (19% at worst); it ranks the one-pass
+    256x128 tile first on large problems, a split last round at
+    4096x11008x4096, and split 32x64..128x128 tiles at M=16..256.
     """
     dims = problem.dims_dict
     m, n, k = dims["M"], dims["N"], dims["K"]
@@ -643,17 +650,22 @@ def gemm_time_estimate(config: KernelConfig, problem: Problem, caps: DeviceCaps)
     split = config.get("SPLIT_K", 1)
     elem = itemsize(problem.dtype)
     tiles = ceil_div(m, bm) * ceil_div(n, bn)
-    programs = tiles * split
-    slices = ceil_div(ceil_div(k, bk), split) + _PIPELINE_FILL_SLICES
+    resident = gemm_resident_workgroups(config, caps, elem)
+    round_ = caps.cu_count * resident
+    # With several rounds of tiles only the last, partial round is split.
+    whole = tiles // round_ * round_ if split > 1 and tiles >= round_ else (0 if split > 1 else tiles)
+    split_programs = (tiles - whole) * split
+    all_slices = ceil_div(k, bk) + _PIPELINE_FILL_SLICES
+    split_slices = ceil_div(ceil_div(k, bk), split) + _PIPELINE_FILL_SLICES
     reuse = min((bm * bn) / (bm + bn), _FULL_RATE_REUSE)
     rate = _CU_FLOPS * math.sqrt(reuse / _FULL_RATE_REUSE)
-    compute = ceil_div(programs, caps.cu_count) * bm * bn * bk * 2 * slices / rate
-    moved = (m * k + k * n + m * n) * elem
-    if split > 1:
-        moved += 2 * programs * bm * bn * 4
+    tile_flops = bm * bn * bk * 2
+    compute = (ceil_div(whole, caps.cu_count) * all_slices
+               + ceil_div(split_programs, caps.cu_count) * split_slices) * tile_flops / rate
+    moved = (m * k + k * n + m * n) * elem + 2 * split_programs * bm * bn * 4 * (split > 1)
     memory = moved / _HBM_BYTES_PER_S
-    resident = gemm_resident_workgroups(config, caps, elem)
-    latency = ceil_div(programs, caps.cu_count * resident) * slices * _SLICE_LATENCY_S
+    latency = (ceil_div(whole, round_) * all_slices
+               + ceil_div(split_programs, round_) * split_slices) * _SLICE_LATENCY_S
     # A 4-norm rather than the plain maximum: the largest bound decides, and a
     # config with slack in the other two ranks ahead of one without.
     return (compute**4 + memory**4 + latency**4) ** 0.25

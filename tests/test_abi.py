@@ -37,7 +37,7 @@ def test_header_declares_the_expected_entry_points():
     assert _declared() == {
         "kf_abi_version", "kf_build_target", "kf_last_error",
         "kf_gemm", "kf_gemm_has_variant", "kf_gemm_variant_count", "kf_gemm_variant_info",
-        "kf_gemm_split_k", "kf_gemm_workspace_bytes",
+        "kf_gemm_split_k", "kf_gemm_workspace_bytes", "kf_gemm_concurrent_tiles",
         "kf_gemv", "kf_gemv_workspace_bytes", "kf_softmax", "kf_rmsnorm",
         "kf_rmsnorm_two_pass", "kf_rmsnorm_two_pass_max_staged_cols", "kf_vector_add",
     }
@@ -140,6 +140,13 @@ def test_gemm_split_k_argument_errors(lib):
     # split_k is only meaningful on the direct pipeline: kf_gemm never splits,
     # and zero-size problems return before the workspace is looked at.
     assert gemm(m=0) == hip.KF_OK and gemm(n=0) == hip.KF_OK
+
+
+def test_concurrent_tiles_query_errors(lib):
+    rc = lib.kf_gemm_concurrent_tiles(7, 256, 128, 64, 8, 3, 1)
+    assert rc == hip.KF_ERR_UNSUPPORTED_DTYPE
+    rc, msg = _rc_and_message(lambda: lib.kf_gemm_concurrent_tiles(1, 48, 128, 64, 8, 3, 1))
+    assert rc == hip.KF_ERR_NOT_BUILT and "no compiled" in msg
 
 
 def test_gemv_argument_errors(lib):

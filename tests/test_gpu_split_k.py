@@ -155,6 +155,45 @@ def test_shared_workspace_serves_any_sequence_of_calls():
             _gate(ops.matmul_ref(a, b), out, torch.float16, f"case {i} round {rnd} {cfg}")
 
 
+@pytest.mark.parametrize("split", (2, 3, 4))
+@pytest.mark.parametrize("fused", (False, True))
+def test_split_k_of_the_last_partial_round(split, fused):
+    """260 tiles of 256x128 (one workgroup per CU): 256 run unsplit, the 4 of
+    the last round split; every tile is finished exactly once."""
+    m, n, k = 1024, 8320, 1032
+    x = _randn(m, k, dtype=torch.float16, seed=20 + split)
+    w = _randn(k, n, dtype=torch.float16, seed=21, scale=k**-0.5)
+    bias = _randn(n, dtype=torch.float16, seed=22) if fused else None
+    out, guard = _split_call(x.to(DEV), w.to(DEV), bias.to(DEV) if fused else None, 256, 128, 8,
+                             split)
+    assert guard and torch.isfinite(out).all()
+    ref = ops.linear_gelu_ref(x, w, bias) if fused else ops.matmul_ref(x, w)
+    _gate(ref, out, torch.float16, f"tail split {split} fused={fused}")
+
+
+def test_concurrent_tiles_on_mi355x():
+    """One 256x128 DMA workgroup per CU (147 KiB of LDS); 32x64 tiles up to
+    four per CU (36 KiB of LDS each; registers may allow fewer)."""
+    lib = hip.load()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert lib.kf_gemm_concurrent_tiles(1, 256, 128, 64, 8, 3, 1) == cus
+    small = lib.kf_gemm_concurrent_tiles(1, 32, 64, 64, 4, 3, 1)
+    assert small % cus == 0 and 1 <= small // cus <= 4
+
+
+def test_split_k_with_only_full_rounds_runs_unsplit():
+    """256 tiles of 256x128 fill exactly one round: nothing is split, so the
+    result is bitwise the unsplit kernel's."""
+    from kernelo_amd.kernels.matmul import matmul
+
+    a = _randn(2048, 1024, dtype=torch.float16, seed=30).to(DEV)
+    b = _randn(1024, 4096, dtype=torch.float16, seed=31, scale=1 / 32).to(DEV)
+    split, _ = _split_call(a, b, None, 256, 128, 8, 4)
+    plain = matmul(a, b, config=KernelConfig("matmul", BLOCK_M=256, BLOCK_N=128, BLOCK_K=64,
+                                             GROUP_M=8, DIRECT=1, num_warps=8, num_stages=3))
+    assert torch.equal(split.to(torch.float16), plain.cpu())
+
+
 def test_split_k_on_a_layout_the_dma_cannot_take_runs_unsplit():
     """Strided A sends the tile to the register-staged fallback, which ignores
     split_k; the result is still whole and correct."""

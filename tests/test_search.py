@@ -142,8 +142,11 @@ def test_flagship_gemm_space_on_mi355x():
     # BM x BN x BK x waves x stages x pipeline, then the split-K DMA tiles:
     # BM x BN x waves x stages x SPLIT_K (2, 4, 8, 16).
     assert result.generated == 4 * 4 * 3 * 2 * 2 * 2 + 4 * 4 * 2 * 2 * 4
-    # 256 tiles of 256x128 already fill the CUs: no split survives.
-    assert not any(c.get("SPLIT_K", 1) > 1 for c in result.candidates)
+    # 256 tiles of 256x128 fill one round of the 256 CUs exactly: the winner
+    # runs unsplit, and no 256x128 split survives.
+    assert result.candidates[0].get("SPLIT_K", 1) == 1
+    assert not any(c.get("SPLIT_K", 1) > 1 and c["BLOCK_M"] * c["BLOCK_N"] == 256 * 128
+                   for c in result.candidates)
     assert len(result.candidates) == DEFAULT_MAX_CANDIDATES
     # Every rejection is attributed to a named rule.
     assert all(":" in reason for _, reason in result.rejected)
@@ -232,7 +235,7 @@ def test_small_problems_prefer_parallelism():
         (64, 11008, 4096, (64, 128), 2, 8),
         (128, 11008, 4096, (128, 128), 2, 8),
         (256, 4096, 11008, (128, 128), 4, 8),
-        (512, 11008, 4096, (256, 128), 1, 8),
+        (4096, 11008, 4096, (256, 128), 2, 8),  # 1376 tiles: the last 96 split
         (2048, 4096, 4096, (256, 128), 1, 8),
         (2048, 11008, 4096, (256, 128), 1, 8),
     ],
