@@ -35,17 +35,21 @@
 // M/N edges clamp rows/columns (results discarded); the partial last k-slice
 // clamps k into range and zeroes its chunks past K after the DMA lands.
 //
-// Split-K: with args.split_k = S > 1 the grid holds S programs per output
-// tile for the tiles from args.full_tiles on (all tiles when it is 0; the
-// tiles before it run one program each, so a launch can split only the
-// tiles of its last, partial round). Program s multiplies k-slices [s*P, (s+1)*P) (P = ceil(slices / S);
-// a trailing range may be short or empty) by moving its operand bases to
-// slice s*P and running the ordinary loop over a K of its own. It publishes
-// its fp32 accumulators to its partial tile in the workspace, in fragment
-// order (lane-contiguous, so the stores coalesce); the last of the S
-// programs to take the tile's ticket adds the S partials in ascending s --
-// the same order whichever program is last, so results are deterministic --
-// applies the epilogue, writes C and returns the ticket to zero.
+// Split-K (stream-K over the split tiles): with args.split_k > 1, tiles
+// [0, args.full_tiles) run one program each and the remaining T tiles are
+// shared out over P = args.tail_programs programs. Their T*slices (tile,
+// k-slice) iterations, tile-major, are cut into P contiguous ranges; program p
+// walks its range segment by segment (a range may end inside one tile and go
+// on in the next), moving its operand bases to each segment's first slice and
+// running the ordinary loop over a K of its own. A segment that is a whole
+// tile writes C directly. Any other segment publishes its fp32 accumulators to
+// one of the program's two partial slots (its first segment, its last), in
+// fragment order so the stores coalesce, and takes the tile's ticket; the
+// last of the tile's programs adds the tile's segments in ascending k -- the
+// same order whichever program is last, so results are deterministic --
+// applies the epilogue, writes C and returns the ticket to zero. With T*S <=
+// P and S dividing the slice count this is the classic split-K into S equal
+// k-ranges per tile.
 #pragma once
 
 #include <type_traits>
@@ -86,6 +90,15 @@ __device__ __forceinline__ const void* uniform_ptr(const void* p) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
   const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
   return reinterpret_cast<const void*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// A wave-uniform 64-bit integer, moved into SGPRs. Values the compiler
+// computes with vector instructions (64-bit division) would otherwise occupy
+// VGPRs for the whole K loop.
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
 // 16 bytes per lane from (sbase + voff) into LDS at lds + 16*lane; sbase and
@@ -178,49 +191,63 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
 
   const int64_t M = args.M, N = args.N;
 
-  // ---- tile order: regroup per XCD, then GROUP_M bands (as gemm_kernel) ----
-  // Tiles [0, full) run one program each; the tiles after them (all tiles
-  // when full is 0) run args.split_k programs each. Each group's programs
-  // are regrouped per XCD on their own, the split ones with s the slowest
-  // index, so one XCD's programs share a k-range and its rows of A.
+  // ---- work: whole tiles, then ranges of k-slices over the split tiles -----
+  // Tiles [0, full) run one program each (every tile when split_k is 1),
+  // regrouped per XCD and into GROUP_M bands. The other T = tiles - full
+  // tiles are shared out over P = args.tail_programs programs: their T*nk
+  // (tile, k-slice) iterations, tile-major, are cut into P contiguous ranges,
+  // program p taking [floor(p*I/P), floor((p+1)*I/P)) with P <= I, so no
+  // range is empty. A range may end inside one tile and go on in the next, so
+  // a program works through one or more segments; a segment that is a whole
+  // tile writes C itself, the others publish an fp32 partial tile for the
+  // tile's last-arriving program.
   const int64_t tiles_m = ceil_div(M, BM);
   const int64_t tiles_n = ceil_div(N, BN);
   const int64_t ntiles = tiles_m * tiles_n;
+  const int64_t nk_all = ceil_div(args.K, static_cast<int64_t>(BK));
   const int64_t full = args.split_k > 1 ? args.full_tiles : ntiles;
-  const int64_t split_tiles = ntiles - full;
-  int64_t pid = blockIdx.x;
-  int split = 1;
-  int s_idx = 0;
-  if (pid < full) {
-    if (full % kNumXcd == 0) pid = (pid % kNumXcd) * (full / kNumXcd) + pid / kNumXcd;
-  } else {
-    split = args.split_k;
-    const int64_t nsplit = split_tiles * split;
-    int64_t q = pid - full;
-    if (nsplit % kNumXcd == 0) q = (q % kNumXcd) * (nsplit / kNumXcd) + q / kNumXcd;
-    s_idx = static_cast<int>(q / split_tiles);
-    pid = full + q % split_tiles;
-  }
-  const int64_t tile = pid;
-  // This program's k-range: slices [kt0, kt0 + P), as a K of its own.
-  const int64_t slices_per = ceil_div(ceil_div(args.K, BK), static_cast<int64_t>(split));
-  const int64_t kt0 = s_idx * slices_per;
-  int64_t K = args.K - kt0 * BK;
-  K = K < slices_per * BK ? K : slices_per * BK;
-  K = K > 0 ? K : 0;
-  const int64_t gm = args.group_m;
-  const int64_t in_group = gm * tiles_n;
-  const int64_t group = pid / in_group;
-  const int64_t first_m = group * gm;
-  const int64_t size_m = (tiles_m - first_m < gm) ? (tiles_m - first_m) : gm;
-  const int64_t m0 = (first_m + (pid % in_group) % size_m) * BM;
-  const int64_t n0 = ((pid % in_group) / size_m) * BN;
+  const int64_t P = args.split_k > 1 ? args.tail_programs : 1;
+  const int64_t I = (ntiles - full) * nk_all;
+  const bool streamed = static_cast<int64_t>(blockIdx.x) >= full;
+  const int64_t prog = streamed ? static_cast<int64_t>(blockIdx.x) - full : 0;
+  const int64_t it_first = uniform64(streamed ? prog * I / P : 0);
+  const int64_t it_end = uniform64(streamed ? (prog + 1) * I / P : 1);  // unsplit: one pass
+  auto owner = [&](int64_t i) { return ((i + 1) * P - 1) / I; };  // program holding iteration i
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / Tl::WN;
   const int wn = wave % Tl::WN;
+
+  for (int64_t it = it_first; it < it_end;) {
+  int64_t pid, kb, ke;
+  if (!streamed) {
+    pid = blockIdx.x;
+    if (full % kNumXcd == 0) pid = (pid % kNumXcd) * (full / kNumXcd) + pid / kNumXcd;
+    kb = 0;
+    ke = nk_all;
+    it = it_end;
+  } else {
+    const int64_t t = uniform64(it / nk_all);
+    kb = it - t * nk_all;
+    ke = kb + (it_end - it) < nk_all ? kb + (it_end - it) : nk_all;
+    pid = full + t;
+    it += ke - kb;
+  }
+  pid = uniform64(pid);
+  const int64_t tile = pid;
+  // This segment's k-range: slices [kb, ke), as a K of its own.
+  const int64_t kt0 = kb;
+  int64_t K = args.K - kt0 * BK;
+  K = K < (ke - kb) * BK ? K : (ke - kb) * BK;
+  const int64_t gm = args.group_m;
+  const int64_t in_group = gm * tiles_n;
+  const int64_t group = pid / in_group;
+  const int64_t first_m = group * gm;
+  const int64_t size_m = (tiles_m - first_m < gm) ? (tiles_m - first_m) : gm;
+  const int64_t m0 = uniform64((first_m + (pid % in_group) % size_m) * BM);
+  const int64_t n0 = uniform64(((pid % in_group) / size_m) * BN);
 
   // ---- DMA sources: tile bases + per-lane byte offsets -----------------------
   // Chunk q = j*NT + tid is written to LDS slot q; its source is the chunk at
@@ -277,12 +304,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   // The partial last slice: k is clamped into range per lane so every source
   // stays inside its operand (K % 8 == 0, so K - 8 >= k0); the chunks past K
   // are zeroed by zero_tail() once the DMA has landed.
+  // Offsets within the slice are 32-bit: `rem` (1..63, a multiple of 8) is
+  // the number of valid k of the partial slice.
   auto issue_last = [&](const char* stage, int64_t kt) {
     const uint32_t la = lds_offset(stage) + lds_lane0;
     const int64_t k0 = kt * BK;
-    int64_t k = k0 + kc;
-    k = k < K ? k : K - 8;
-    const uint32_t dk = static_cast<uint32_t>((k - k0) * 2) - static_cast<uint32_t>(kc * 2);
+    const int rem = static_cast<int>(K - k0);
+    const int k = kc < rem ? kc : rem - 8;
+    const uint32_t dk = static_cast<uint32_t>(k * 2) - static_cast<uint32_t>(kc * 2);
     const char* ab = a_tile + k0 * 2;
 #pragma unroll
     for (int j = 0; j < Tl::kAIters; ++j) dma16(ab, a_off[j] + dk, la + j * NT * 16);
@@ -290,10 +319,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
       const char* bb = b_tile + k0 * ldb_b;
 #pragma unroll
       for (int j = 0; j < Tl::kBIters; ++j) {
-        int64_t kb = k0 + b_row[j];
-        kb = kb < K ? kb : K - 1;
+        const int kb = b_row[j] < rem ? b_row[j] : rem - 1;
         const uint32_t off = b_off[j] - static_cast<uint32_t>(b_row[j] * ldb_b) +
-                             static_cast<uint32_t>((kb - k0) * ldb_b);
+                             static_cast<uint32_t>(kb * ldb_b);
         dma16(bb, off, la + Tl::kABytes + j * NT * 16);
       }
     } else {
@@ -311,15 +339,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   // Zero the chunks of slice kt that lie past K (after its DMA landed).
   auto fix = [&](char* stage, int64_t kt) {
     if (!(ktail && kt == nk - 1)) return;
-    const int64_t k0 = kt * BK;
+    const int rem = static_cast<int>(K - kt * BK);
     const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int j = 0; j < Tl::kAIters; ++j)
-      if (k0 + kc >= K) *reinterpret_cast<u32x4*>(stage + (j * NT + tid) * 16) = z;
+      if (kc >= rem) *reinterpret_cast<u32x4*>(stage + (j * NT + tid) * 16) = z;
 #pragma unroll
     for (int j = 0; j < Tl::kBIters; ++j) {
-      const int64_t kk = BLAYOUT == 0 ? k0 + b_row[j] : k0 + kc;
-      if (kk >= K) *reinterpret_cast<u32x4*>(stage + Tl::kABytes + (j * NT + tid) * 16) = z;
+      const int kk = BLAYOUT == 0 ? b_row[j] : kc;
+      if (kk >= rem) *reinterpret_cast<u32x4*>(stage + Tl::kABytes + (j * NT + tid) * 16) = z;
     }
   };
 
@@ -483,20 +511,21 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
     }
   }
 
-  // ---- split-K: publish the partial tile; the last program sums them -------
-  if (split > 1) {
+  // ---- partial segments: publish; the tile's last program sums them -------
+  if (!(kb == 0 && ke == nk_all)) {
     // Partials move through agent-scope (sc1) stores and loads, which are
     // coherent across XCDs without writing back or invalidating whole L2s;
     // the only ordering needed is that every lane's stores have completed
     // (vmcnt(0), then the workgroup barrier) before the ticket is taken.
-    // Fragment (i, j) of lane tid is the 16 bytes at ((i*FN + j)*NT + tid)*16.
+    // Program q keeps two partial slots: 2q for its first segment, 2q + 1
+    // for its last (middle segments are whole tiles). Fragment (i, j) of lane
+    // tid is the 16 bytes at ((i*FN + j)*NT + tid)*16 of a slot.
     constexpr int kTileFloats = BM * BN;
     const int64_t st = tile - full;  // index among the split tiles
-    auto part = [&](int q) {
-      return tile_rsrc(args.ws + (static_cast<int64_t>(q) * split_tiles + st) * kTileFloats,
-                       kTileFloats * 4);
+    auto slot = [&](int64_t q, bool first) {
+      return tile_rsrc(args.ws + (2 * q + (first ? 0 : 1)) * kTileFloats, kTileFloats * 4);
     };
-    const __amdgpu_buffer_rsrc_t mine = part(s_idx);
+    const __amdgpu_buffer_rsrc_t mine = slot(prog, st * nk_all + kb == it_first);
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -507,31 +536,37 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
     wait_vm<0>();  // this lane's partial stores are done
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     // The K loop ended on a barrier, so the stage buffers are free: the
-    // ticket is broadcast through the first word of LDS.
+    // ticket is broadcast through the first word of LDS, and every wave has
+    // read it before any starts the next segment's DMA.
     unsigned* const ticket = reinterpret_cast<unsigned*>(lds);
     __syncthreads();
     if (tid == 0)
       *ticket = __hip_atomic_fetch_add(&args.tickets[st], 1u, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    if (*ticket != static_cast<unsigned>(split - 1)) return;
+    const unsigned arrived = *ticket;
+    __syncthreads();
+    const int64_t q0 = owner(st * nk_all);
+    const int64_t q1 = owner((st + 1) * nk_all - 1);
+    if (arrived != static_cast<unsigned>(q1 - q0)) continue;
+    // Last of the tile's programs: add the segments in ascending k.
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int q = 0; q < split; ++q) {
-      const __amdgpu_buffer_rsrc_t src = part(q);
-      u32x4 p[FM][FN];  // all of slice q's loads in flight before the first add
+    for (int64_t q = q0; q <= q1; ++q) {
+      const __amdgpu_buffer_rsrc_t src = slot(q, (q * I / P) / nk_all == st);
+      u32x4 pv[FM][FN];  // all of segment q's loads in flight before the first add
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          p[i][j] = __builtin_amdgcn_raw_buffer_load_b128(src, ((i * FN + j) * NT + tid) * 16, 0,
-                                                          kCachePolicySc1);
+          pv[i][j] = __builtin_amdgcn_raw_buffer_load_b128(src, ((i * FN + j) * NT + tid) * 16, 0,
+                                                           kCachePolicySc1);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] += __builtin_bit_cast(f32x4, p[i][j]);
+        for (int j = 0; j < FN; ++j) acc[i][j] += __builtin_bit_cast(f32x4, pv[i][j]);
     }
     if (tid == 0) __hip_atomic_store(&args.tickets[st], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -557,6 +592,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
       }
     }
   }
+  }  // segments
 }
 
 }  // namespace gemm

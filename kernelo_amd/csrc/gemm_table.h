@@ -16,12 +16,14 @@ struct Args {
   int64_t lda_m, lda_k, ldb_k, ldb_n, ldc_m, ldc_n;
   int epilogue;
   int group_m;
-  // Split-K (DMA pipeline only): tiles [full_tiles, tiles) run split_k
-  // programs each, every one over a contiguous range of k-slices; ws holds
-  // their fp32 partial tiles and tickets one counter per split tile (zero
-  // between launches). split_k == 1 leaves full_tiles, ws and tickets unused.
+  // Split-K (DMA pipeline only). With split_k > 1, tiles [0, full_tiles) run
+  // one program each and the (tile, k-slice) iterations of the other tiles
+  // are cut into tail_programs contiguous ranges, one program each; ws holds
+  // two fp32 partial tiles per such program and tickets one counter per split
+  // tile (zero between launches). split_k == 1 leaves the rest unused.
   int split_k;
   int64_t full_tiles;
+  int64_t tail_programs;
   float* ws;
   unsigned* tickets;
 };

@@ -78,8 +78,9 @@ def test_workspace_sizing(lib):
     assert lib.kf_gemv_workspace_bytes(1, 11008, 8) == counters + 8 * 11008 * 4
     assert lib.kf_gemv_workspace_bytes(0, 11008, 8) == 0
     tiles = 1 * (11008 // 64)
-    assert lib.kf_gemm_workspace_bytes(32, 11008, 32, 64, 4) == counters + 4 * tiles * 32 * 64 * 4
-    assert lib.kf_gemm_workspace_bytes(30, 11000, 32, 64, 4) == counters + 4 * tiles * 32 * 64 * 4
+    # Two partial tiles per split program, at most split_k programs per tile.
+    assert lib.kf_gemm_workspace_bytes(32, 11008, 32, 64, 4) == counters + 2 * 4 * tiles * 32 * 64 * 4
+    assert lib.kf_gemm_workspace_bytes(30, 11000, 32, 64, 4) == counters + 2 * 4 * tiles * 32 * 64 * 4
     assert lib.kf_gemm_workspace_bytes(32, 11008, 32, 64, 1) == 0
     assert lib.kf_gemm_workspace_bytes(0, 11008, 32, 64, 4) == 0
 

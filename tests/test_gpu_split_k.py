@@ -171,6 +171,22 @@ def test_split_k_of_the_last_partial_round(split, fused):
     _gate(ref, out, torch.float16, f"tail split {split} fused={fused}")
 
 
+@pytest.mark.parametrize("split", (3, 4, 8))
+def test_last_round_shared_out_in_ranges_that_cross_tiles(split):
+    """344 tiles of 256x128: 256 unsplit, the last 88 shared out over one
+    round of 256 programs, 88*16/256 = 5.5 k-slices each, so most ranges end
+    inside one tile and go on in the next."""
+    m, n, k = 1024, 11008, 1024
+    x = _randn(m, k, dtype=torch.float16, seed=40 + split)
+    w = _randn(k, n, dtype=torch.float16, seed=41, scale=k**-0.5)
+    bias = _randn(n, dtype=torch.float16, seed=42)
+    out, guard = _split_call(x.to(DEV), w.to(DEV), bias.to(DEV), 256, 128, 8, split)
+    assert guard and torch.isfinite(out).all()
+    _gate(ops.linear_gelu_ref(x, w, bias), out, torch.float16, f"stream-K tail split {split}")
+    again, _ = _split_call(x.to(DEV), w.to(DEV), bias.to(DEV), 256, 128, 8, split)
+    assert torch.equal(out, again)
+
+
 def test_concurrent_tiles_on_mi355x():
     """One 256x128 DMA workgroup per CU (147 KiB of LDS); 32x64 tiles up to
     four per CU (36 KiB of LDS each; registers may allow fewer)."""
