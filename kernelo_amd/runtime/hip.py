@@ -133,6 +133,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "kf_vector_add": (_int, [_int, _vp, _vp, _vp, _i64, _int, _int, _vp]),
 }
 
+#: kf_abi_version() of the library these signatures describe.
+ABI_VERSION = 4
+
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
 
@@ -155,6 +158,12 @@ def load(path: str | Path | None = None) -> ctypes.CDLL:
             lib = ctypes.CDLL(str(target))
         except OSError as exc:
             raise KernelLibraryNotCompiled(f"cannot load {target}: {exc}") from exc
+        version = lib.kf_abi_version()
+        if version != ABI_VERSION:
+            raise KernelLibraryNotCompiled(
+                f"{target} has ABI version {version}, this package binds version {ABI_VERSION}; "
+                "rebuild it with `python -m kernelo_amd.build`"
+            )
         for name, (restype, argtypes) in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.restype = restype

@@ -51,8 +51,22 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_identification(lib):
-    assert lib.kf_abi_version() == 4
+    assert lib.kf_abi_version() == hip.ABI_VERSION == 4
     assert lib.kf_build_target() == b"gfx950"
+
+
+def test_a_library_of_another_abi_version_is_refused(tmp_path):
+    import shutil
+    import subprocess
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    src = tmp_path / "old.c"
+    src.write_text("int kf_abi_version(void) { return 3; }\n")
+    so = tmp_path / "libold.so"
+    subprocess.run(["gcc", "-shared", "-fPIC", "-o", str(so), str(src)], check=True)
+    with pytest.raises(hip.KernelLibraryNotCompiled, match="ABI version 3"):
+        hip.load(so)
 
 
 def test_variant_table_equals_the_instantiation_rules(lib):
