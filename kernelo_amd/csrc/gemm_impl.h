@@ -46,8 +46,12 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ float gelu_tanh(float a) {
   // 0.5a(1 + tanh(z)) with tanh(z) = 2/(1+exp(-2z)) - 1  =>  a / (1 + exp(-2z)).
+  // The quotient uses the hardware reciprocal (v_rcp_f32, 1 ulp) rather than
+  // the IEEE division sequence: the result is rounded to the output dtype and
+  // gated at 5e-3 (16-bit) or 1e-5 (fp32), and rcp(inf) = 0 keeps the
+  // saturated negative tail at -0.
   const float inner = kGeluC * (a + 0.044715f * a * a * a);
-  return a / (1.0f + __builtin_amdgcn_exp2f(-inner * kLog2e));
+  return a * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-inner * kLog2e));
 }
 
 template <typename T>
