@@ -24,7 +24,7 @@ struct Raw<2> { using type = uint16_t; };
 template <>
 struct Raw<4> { using type = uint32_t; };
 template <>
-struct Raw<8> { using type = uint2; };
+struct Raw<8> { using type = uint32_t __attribute__((ext_vector_type(2))); };
 template <>
 struct Raw<16> { using type = u32x4; };
 
@@ -46,8 +46,8 @@ __global__ __launch_bounds__(1024) void vector_add_kernel(const T* __restrict__ 
     R ra[NL], rb[NL];
 #pragma unroll
     for (int j = 0; j < NL; ++j) {
-      ra[j] = *reinterpret_cast<const R*>(a + at(j));
-      rb[j] = *reinterpret_cast<const R*>(b + at(j));
+      ra[j] = load_once(reinterpret_cast<const R*>(a + at(j)));
+      rb[j] = load_once(reinterpret_cast<const R*>(b + at(j)));
     }
 #pragma unroll
     for (int j = 0; j < NL; ++j) {

@@ -211,7 +211,7 @@ __global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_splitk(
         for (int m = 0; m < MR; ++m) xt[u][m] = xrow[m][(kk + u * step) * ldx_k];
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        raw[u] = *reinterpret_cast<const u32x4*>(wcol + (kk + u * step) * ldw_k);
+        raw[u] = load_once(reinterpret_cast<const u32x4*>(wcol + (kk + u * step) * ldw_k));
     };
     auto use_trip = [&](const T (&xt)[U][MR], const u32x4 (&raw)[U]) {
 #pragma unroll
@@ -251,7 +251,7 @@ __global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_splitk(
       float xv[MR];
 #pragma unroll
       for (int m = 0; m < MR; ++m) xv[m] = to_f32(xrow[m][k * ldx_k]);
-      const u32x4 raw = *reinterpret_cast<const u32x4*>(wcol + k * ldw_k);
+      const u32x4 raw = load_once(reinterpret_cast<const u32x4*>(wcol + k * ldw_k));
       T w[V];
       __builtin_memcpy(w, &raw, 16);
       fma_row(xv, w);
@@ -348,7 +348,7 @@ __global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_dot(
     u32x4 wr[U];
     u32x4 xr[U][MR];
 #pragma unroll
-    for (int u = 0; u < U; ++u) wr[u] = *reinterpret_cast<const u32x4*>(wcol + k + u * kStep);
+    for (int u = 0; u < U; ++u) wr[u] = load_once(reinterpret_cast<const u32x4*>(wcol + k + u * kStep));
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -363,7 +363,7 @@ __global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_dot(
     u32x4 xr[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) xr[m] = *reinterpret_cast<const u32x4*>(xrow[m] + k);
-    dot8(xr, *reinterpret_cast<const u32x4*>(wcol + k));
+    dot8(xr, load_once(reinterpret_cast<const u32x4*>(wcol + k)));
   }
 
   // The LPR lanes of a column: butterfly over the low lane bits.
