@@ -589,11 +589,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   // pieces: 8 stores per lane for a 256x128 tile instead of 64 two-byte
   // ones, whose per-lane addressing held the tile's last round back
   // (4096x11008x4096: 387 -> 354 us). Other layouts store element by element.
-  const bool stage_c = args.ldc_n == 1 && (args.ldc_m * 2) % 16 == 0 &&
+  constexpr int kPitch = BN + 8;  // elements per LDS row of the staged C: 16 bytes of padding
+  constexpr bool kCFits = BM * kPitch * 2 <= Tl::kLdsBytes;
+  const bool stage_c = kCFits && args.ldc_n == 1 && (args.ldc_m * 2) % 16 == 0 &&
                        (reinterpret_cast<uintptr_t>(C) & 15u) == 0;
   if (stage_c) {
-    constexpr int kPitch = BN + 8;  // elements per LDS row: 16 bytes of padding
-    static_assert(BM * kPitch * 2 <= Tl::kLdsBytes, "the C tile must fit the stage buffers");
     T* const ct = reinterpret_cast<T*>(lds);
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
