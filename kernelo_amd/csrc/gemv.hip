@@ -33,6 +33,16 @@ namespace {
 
 constexpr int kGemvMaxWaves = 16;
 constexpr size_t kGemvMaxLds = 64 * 1024;  // dynamic LDS without an opt-in attribute
+
+// B bytes loaded as one vector (B = 4, 8, 16) or two 16-byte vectors (32).
+template <int B> struct XChunkT;
+template <> struct XChunkT<4> { using type = uint32_t; };
+template <> struct XChunkT<8> { using type = uint32_t __attribute__((ext_vector_type(2))); };
+template <> struct XChunkT<16> { using type = u32x4; };
+struct U32x8 { u32x4 lo, hi; };
+template <> struct XChunkT<32> { using type = U32x8; };
+template <int B>
+using XChunk = typename XChunkT<B>::type;
 constexpr float kGeluC = 1.5957691216057308f;  // 2*sqrt(2/pi)
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -199,52 +209,85 @@ __global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_splitk(
   int64_t k = kbeg + wave * RPW + sub;
   if (vec_path) {
     const T* wcol = W + col_ld;
-    // U rows per lane per trip. The x values go first so that the wait for
-    // them does not also wait for the W rows behind them; then all W loads
-    // issue back to back and are consumed in order. Trips are double
-    // buffered: the next trip's loads are in flight while this one is
-    // multiplied, so a wave streams without a latency gap between trips.
-    auto load_trip = [&](int64_t kk, T (&xt)[U][MR], u32x4 (&raw)[U]) {
+    // A trip covers U*step rows; the lane owns U adjacent ones at lane_row,
+    // so its x values of a trip are U adjacent elements of each x row: one
+    // vector load per row when x is k-contiguous and aligned, instead of U
+    // element loads beside the U W loads. Every lane runs the same number of
+    // whole trips; the rows after them take the per-row loop below.
+    // The x values go first so that the wait for them does not also wait for
+    // the W rows behind them; then all W loads issue back to back and are
+    // consumed in order. Trips are double buffered: the next trip's loads are
+    // in flight while this one is multiplied, so a wave streams without a
+    // latency gap between trips.
+    const int64_t trip = U * step;
+    const int64_t ntrips = (kend - kbeg) / trip;
+    const int64_t lane_row = kbeg + static_cast<int64_t>(wave * RPW + sub) * U;
+    constexpr int kXBytes = U * static_cast<int>(sizeof(T));
+    bool xvec = ldx_k == 1 && kbeg % U == 0;
 #pragma unroll
-      for (int u = 0; u < U; ++u)
+    for (int m = 0; m < MR; ++m)
+      xvec = xvec && reinterpret_cast<uintptr_t>(xrow[m]) % kXBytes == 0;
+    auto run_trips = [&](auto xvec_tag) {
+      constexpr bool XV = decltype(xvec_tag)::value;
+      auto load_trip = [&](int64_t kk, T (&xt)[U][MR], u32x4 (&raw)[U]) {
 #pragma unroll
-        for (int m = 0; m < MR; ++m) xt[u][m] = xrow[m][(kk + u * step) * ldx_k];
+        for (int m = 0; m < MR; ++m) {
+          if constexpr (XV) {
+            XChunk<kXBytes> c = *reinterpret_cast<const XChunk<kXBytes>*>(xrow[m] + kk);
+            T e[U];
+            __builtin_memcpy(e, &c, kXBytes);
 #pragma unroll
-      for (int u = 0; u < U; ++u)
-        raw[u] = load_once(reinterpret_cast<const u32x4*>(wcol + (kk + u * step) * ldw_k));
-    };
-    auto use_trip = [&](const T (&xt)[U][MR], const u32x4 (&raw)[U]) {
+            for (int u = 0; u < U; ++u) xt[u][m] = e[u];
+          } else {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        float xv[MR];
+            for (int u = 0; u < U; ++u) xt[u][m] = xrow[m][(kk + u) * ldx_k];
+          }
+        }
 #pragma unroll
-        for (int m = 0; m < MR; ++m) xv[m] = to_f32(xt[u][m]);
-        T w[V];
-        __builtin_memcpy(w, &raw[u], 16);
-        fma_row(xv, w);
+        for (int u = 0; u < U; ++u)
+          raw[u] = load_once(reinterpret_cast<const u32x4*>(wcol + (kk + u) * ldw_k));
+      };
+      auto use_trip = [&](const T (&xt)[U][MR], const u32x4 (&raw)[U]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          float xv[MR];
+#pragma unroll
+          for (int m = 0; m < MR; ++m) xv[m] = to_f32(xt[u][m]);
+          T w[V];
+          __builtin_memcpy(w, &raw[u], 16);
+          fma_row(xv, w);
+        }
+      };
+      T xa[U][MR], xb[U][MR];
+      u32x4 ra[U], rb[U];
+      if (ntrips > 0) load_trip(lane_row, xa, ra);
+      int64_t t = 0;
+      // The scheduling barriers keep each trip's loads ahead of the previous
+      // trip's multiplies: without them the scheduler converts each value
+      // right after its load and waits for it, serialising the memory
+      // latencies.
+      for (; t + 1 < ntrips; t += 2) {
+        load_trip(lane_row + (t + 1) * trip, xb, rb);
+        __builtin_amdgcn_sched_barrier(0);
+        use_trip(xa, ra);
+        if (t + 2 < ntrips) load_trip(lane_row + (t + 2) * trip, xa, ra);
+        __builtin_amdgcn_sched_barrier(0);
+        use_trip(xb, rb);
+      }
+      if (t < ntrips) {
+        __builtin_amdgcn_sched_barrier(0);
+        use_trip(xa, ra);
       }
     };
-    const int64_t trip = U * step;
-    const int64_t span = kend - k - (U - 1) * step;  // trips t with k + t*trip + (U-1)*step < kend
-    const int64_t ntrips = span > 0 ? ceil_div(span, trip) : 0;
-    T xa[U][MR], xb[U][MR];
-    u32x4 ra[U], rb[U];
-    if (ntrips > 0) load_trip(k, xa, ra);
-    int64_t t = 0;
-    // The scheduling barriers keep each trip's loads ahead of the previous
-    // trip's multiplies: without them the scheduler converts each value right
-    // after its load and waits for it, serialising the memory latencies.
-    for (; t + 1 < ntrips; t += 2) {
-      load_trip(k + (t + 1) * trip, xb, rb);
-      __builtin_amdgcn_sched_barrier(0);
-      use_trip(xa, ra);
-      if (t + 2 < ntrips) load_trip(k + (t + 2) * trip, xa, ra);
-      __builtin_amdgcn_sched_barrier(0);
-      use_trip(xb, rb);
-    }
-    if (t < ntrips) {
-      __builtin_amdgcn_sched_barrier(0);
-      use_trip(xa, ra);
+    if constexpr (gemv_max_lanes<MR>() < 1024) {
+      if (xvec)
+        run_trips(std::true_type{});
+      else
+        run_trips(std::false_type{});
+    } else {
+      // 1024-lane workgroups have 128 registers per lane: one loop body only.
+      (void)xvec;
+      run_trips(std::false_type{});
     }
     k += ntrips * trip;
     for (; k < kend; k += step) {

@@ -303,6 +303,31 @@ def test_gemv_decode_config(split, warps, lanes):
     _gate(ops.matmul_ref(x, w), out, torch.bfloat16, str(cfg))
 
 
+@pytest.mark.parametrize("layout", ("contiguous", "k_strided", "offset"))
+@pytest.mark.parametrize("m", (1, 2, 3))
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("k,split", ((4096, 4), (4097, 3), (1000, 1)))
+def test_gemv_x_layouts(layout, m, dtype, k, split):
+    """x rows loaded as one vector per trip (k-contiguous, aligned slice starts)
+    or element by element (strided or misaligned x, slices starting off a
+    multiple of the trip's rows), plus the rows after the last whole trip."""
+    from kernelo_amd.kernels.matmul import matmul
+
+    x = _randn(m, k, dtype=dtype, seed=k + m)
+    w = _randn(k, 2056, dtype=dtype, seed=7, scale=k**-0.5)
+    if layout == "contiguous":
+        dx = x.to(DEV)
+    elif layout == "k_strided":
+        dx = torch.zeros(m, 2 * k, dtype=dtype, device=DEV)[:, ::2]
+        dx.copy_(x.to(DEV))
+    else:
+        dx = torch.zeros(m, k + 1, dtype=dtype, device=DEV)[:, 1:]
+        dx.copy_(x.to(DEV))
+    cfg = KernelConfig("matmul", GEMV=1, SPLIT_K=split, LANES_PER_ROW=32, num_warps=4)
+    out = matmul(dx, w.to(DEV), config=cfg)
+    _gate(ops.matmul_ref(x, w), out, dtype, f"{layout} m={m} k={k} split={split}")
+
+
 def test_gemv_is_deterministic():
     from kernelo_amd.kernels.matmul import matmul
 
