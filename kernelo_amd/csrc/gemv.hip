@@ -34,6 +34,14 @@ namespace {
 constexpr int kGemvMaxWaves = 16;
 constexpr size_t kGemvMaxLds = 64 * 1024;  // dynamic LDS without an opt-in attribute
 
+// A wave-uniform 64-bit value held in scalar registers.
+__device__ __forceinline__ int64_t wave_uniform(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi =
+      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // B bytes loaded as one vector (B = 4, 8, 16) or two 16-byte vectors (32).
 template <int B> struct XChunkT;
 template <> struct XChunkT<4> { using type = uint32_t; };
@@ -176,10 +184,17 @@ __global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_splitk(
   const int64_t nb = blockIdx.x;
   const int64_t col0 = nb * BN + cv;
   const int s = blockIdx.y;
-  const int64_t kc = ceil_div(K, split_k);
-  const int64_t kbeg = static_cast<int64_t>(s) * kc;
-  const int64_t kend = (kbeg + kc < K) ? kbeg + kc : K;
   const int64_t step = static_cast<int64_t>(nwaves) * RPW;  // row groups
+  // Slices are cut on whole trips of U*step rows, shared out as evenly as
+  // whole trips allow: every slice starts on a trip (so x is read as vectors)
+  // and only the last one can end in a partial trip. Slices past the last
+  // trip are empty and publish zeros.
+  const int64_t trip_rows = static_cast<int64_t>(U) * step;
+  const int64_t ntr = ceil_div(K, trip_rows);
+  const int64_t tb = static_cast<int64_t>(s) * ntr / split_k;
+  const int64_t te = static_cast<int64_t>(s + 1) * ntr / split_k;
+  const int64_t kbeg = wave_uniform((tb * trip_rows < K) ? tb * trip_rows : K);
+  const int64_t kend = wave_uniform((te * trip_rows < K) ? te * trip_rows : K);
   // With aligned rows and N a multiple of V every lane's vector is either
   // wholly inside [0, N) or wholly past it. Lanes past N load a clamped,
   // valid vector whose sums are never stored, so one branch-free loop serves
