@@ -34,6 +34,20 @@ namespace {
 constexpr int kGemvMaxWaves = 16;
 constexpr size_t kGemvMaxLds = 64 * 1024;  // dynamic LDS without an opt-in attribute
 
+// One x row of a 16-bit type takes the packed-dot trip (U = 8 rows, even).
+template <typename T, int MR>
+constexpr bool kPackedDot = MR == 1 && sizeof(T) == 2;
+
+// a.lo*b.lo + a.hi*b.hi + c over two packed 16-bit values, in fp32.
+template <typename T>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  typedef T pair __attribute__((ext_vector_type(2)));
+  if constexpr (std::is_same<T, bf16>::value)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(pair, a), __builtin_bit_cast(pair, b), c, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(pair, a), __builtin_bit_cast(pair, b), c, false);
+}
+
 // A wave-uniform 64-bit value held in scalar registers.
 __device__ __forceinline__ int64_t wave_uniform(int64_t v) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
@@ -263,6 +277,26 @@ __global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_splitk(
           raw[u] = load_once(reinterpret_cast<const u32x4*>(wcol + (kk + u) * ldw_k));
       };
       auto use_trip = [&](const T (&xt)[U][MR], const u32x4 (&raw)[U]) {
+        if constexpr (kPackedDot<T, MR>) {
+          // Rows u and u+1 in pairs: for each 32-bit word of the two W
+          // vectors, v_perm_b32 gathers each column's two rows into one
+          // register and v_dot2 multiplies the pair by the x pair in fp32.
+          // Two instructions per two elements instead of two conversions
+          // and two FMAs.
+#pragma unroll
+          for (int u = 0; u < U; u += 2) {
+            const uint32_t xp = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, xt[u][0])) |
+                                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, xt[u + 1][0])) << 16);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const uint32_t w0 = raw[u][j], w1 = raw[u + 1][j];
+              acc[0][2 * j] = dot2<T>(__builtin_amdgcn_perm(w1, w0, 0x05040100u), xp, acc[0][2 * j]);
+              acc[0][2 * j + 1] =
+                  dot2<T>(__builtin_amdgcn_perm(w1, w0, 0x07060302u), xp, acc[0][2 * j + 1]);
+            }
+          }
+          return;
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           float xv[MR];
