@@ -164,7 +164,11 @@ int kf_gemm_variant_info(int index, int* dtype, int* block_m, int* block_n, int*
  * (kernels/matmul.py:132-155, tuning/search.py:377-386); this is its
  * HBM-bound replacement. A workgroup of `waves` wavefronts owns a strip of
  * lanes_per_row (8, 16, 32 or 64) 16-byte vectors of columns and one of
- * `split_k` slices of K. When W is k-contiguous (ldw_k == 1, e.g.
+ * `split_k` slices of K. For n-contiguous W the slices are cut on whole
+ * trips (the rows a workgroup reads in one double-buffered step:
+ * U*64/lanes_per_row per wave, U = 8 for one x row, 4 for two, 2 for three
+ * to eight) and shared out as evenly as whole trips allow, so a split_k above
+ * the number of trips leaves some slices empty. When W is k-contiguous (ldw_k == 1, e.g.
  * nn.Linear's weight passed as weight.t()) with x k-contiguous, 16-byte
  * aligned rows and K a multiple of 16 bytes' worth of elements, the
  * lanes_per_row lanes split one column's k-run instead, 64/lanes_per_row
