@@ -160,18 +160,18 @@ def main(argv: list[str] | None = None) -> int:
     import numpy as np
     import torch
 
-    from kernelo_amd.benchmark import metrics
-    from kernelo_amd.benchmark.runner import flush_buffer
-    from kernelo_amd.kernels.fused_linear import fused_linear_gelu, linear_gelu_reference
-    from kernelo_amd.kernels.matmul import matmul
-    from kernelo_amd.kernels.rmsnorm import rmsnorm, rmsnorm_reference
-    from kernelo_amd.kernels.softmax import softmax
-    from kernelo_amd.runtime.env import device_caps, host_cores
-    from kernelo_amd.testing import assert_verified, exact_fp32_matmul
+    from kernelforge.benchmark import metrics
+    from kernelforge.benchmark.runner import flush_buffer
+    from kernelforge.kernels.fused_linear import fused_linear_gelu, linear_gelu_reference
+    from kernelforge.kernels.matmul import matmul
+    from kernelforge.kernels.rmsnorm import rmsnorm, rmsnorm_reference
+    from kernelforge.kernels.softmax import softmax
+    from kernelforge.runtime.env import device_caps, host_cores
+    from kernelforge.testing import assert_verified, exact_fp32_matmul
 
-    from kernelo_amd.kernels import get_operator
-    from kernelo_amd.runtime.dispatch import select_config
-    from kernelo_amd.tuning.config import Problem
+    from kernelforge.kernels import get_operator
+    from kernelforge.runtime.dispatch import select_config
+    from kernelforge.tuning.config import Problem
 
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
@@ -330,7 +330,7 @@ def main(argv: list[str] | None = None) -> int:
     del cp
 
     # --- widened rows: vector_add (the HBM probe) and the two-pass RMSNorm --------
-    from kernelo_amd.kernels.vector_add import vector_add
+    from kernelforge.kernels.vector_add import vector_add
 
     VN = 1 << 26
     va = torch.randn(VN, generator=g).to(dev)

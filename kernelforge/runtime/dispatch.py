@@ -1,0 +1,75 @@
+"""Configuration selection at call time (kernelforge/runtime/dispatch.py:47-64).
+
+    hit  -> the configuration tuning chose for this device and shape
+    miss -> the operator's default, with the miss reported
+
+Nothing here tunes: tuning is an explicit step (``tune``) whose output this
+reads in microseconds.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from kernelforge.kernels.base import Operator
+from kernelforge.runtime.env import device_key as resolve_device_key
+from kernelforge.tuning.cache import PACKAGED_CACHE, ConfigCache
+from kernelforge.tuning.config import KernelConfig, Problem
+
+SOURCE_CACHE = "cache"
+SOURCE_PACKAGED = "packaged"
+SOURCE_DEFAULT = "default"
+
+
+@dataclass(frozen=True)
+class Selection:
+    config: KernelConfig
+    source: str
+    device_key: str
+
+    @property
+    def tuned(self) -> bool:
+        return self.source in (SOURCE_CACHE, SOURCE_PACKAGED)
+
+    def describe(self) -> str:
+        if self.source == SOURCE_CACHE:
+            return f"tuned configuration for {self.device_key}"
+        if self.source == SOURCE_PACKAGED:
+            return f"packaged tuned configuration for {self.device_key}"
+        return f"default configuration (no cache entry for {self.device_key})"
+
+
+_PACKAGED: ConfigCache | None = None
+
+
+def packaged_cache() -> ConfigCache | None:
+    """The winners shipped with the package (read-only), if present."""
+    global _PACKAGED
+    if _PACKAGED is None and PACKAGED_CACHE.exists():
+        _PACKAGED = ConfigCache(PACKAGED_CACHE)
+    return _PACKAGED
+
+
+def select_config(
+    operator: Operator,
+    problem: Problem,
+    *,
+    cache: ConfigCache | None = None,
+    device: torch.device | str | None = None,
+    use_packaged: bool = True,
+) -> Selection:
+    """Pick the configuration to run ``problem`` with: the user's cache, then
+    the packaged MI355X winners, then the operator default."""
+    key = resolve_device_key(device)
+    resolved = cache if cache is not None else ConfigCache()
+    cached = resolved.get(problem, key)
+    if cached is not None:
+        return Selection(config=cached, source=SOURCE_CACHE, device_key=key)
+    shipped = packaged_cache() if use_packaged else None
+    if shipped is not None:
+        hit = shipped.get(problem, key)
+        if hit is not None:
+            return Selection(config=hit, source=SOURCE_PACKAGED, device_key=key)
+    return Selection(config=operator.default_config(problem), source=SOURCE_DEFAULT, device_key=key)

@@ -1,4 +1,4 @@
-"""CPU oracle for the kernelo_amd hot path -- TEST INFRASTRUCTURE ONLY.
+"""CPU oracle for the kernelforge hot path -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
 import this module, and only as the checker (or the timed CPU baseline),

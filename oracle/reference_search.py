@@ -1,6 +1,6 @@
 """Restatement of the reference's CUDA-era candidate rules -- TEST INFRASTRUCTURE ONLY.
 
-Purpose: pin the *generic* candidate pipeline of kernelo_amd.tuning.search
+Purpose: pin the *generic* candidate pipeline of kernelforge.tuning.search
 (enumerate -> named rejections -> conditional utilisation prune -> priority
 sort -> budget) against numbers the reference publishes. The reference's
 GEMM space on A100 properties yields 432 grid points, 180 feasible, 180 after
@@ -13,7 +13,7 @@ tile-too-small / 30 uncoalesced-B / 27 per-warp / 9 register pressure
 The rules below follow kernelforge/tuning/search.py:259-419 (grid :285-297,
 shared-memory model :299-329, rules :340-394, priority :396-419) and are fed
 through the product's own ``SearchSpace.generate``. They are not product
-code: the product's gfx950 rules live in kernelo_amd/tuning/search.py.
+code: the product's gfx950 rules live in kernelforge/tuning/search.py.
 """
 
 from __future__ import annotations
@@ -21,10 +21,10 @@ from __future__ import annotations
 from collections.abc import Iterator
 from itertools import product
 
-from kernelo_amd.dtypes import itemsize
-from kernelo_amd.runtime.env import DeviceCaps
-from kernelo_amd.tuning.config import KernelConfig, Problem
-from kernelo_amd.tuning.search import SearchSpace, ceil_div
+from kernelforge.dtypes import itemsize
+from kernelforge.runtime.env import DeviceCaps
+from kernelforge.tuning.config import KernelConfig, Problem
+from kernelforge.tuning.search import SearchSpace, ceil_div
 
 # search.py:49-67 (constants)
 MAX_ACC_REGS_PER_THREAD = 128

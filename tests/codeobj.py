@@ -1,4 +1,4 @@
-"""Read the gfx950 code objects inside libkernelo_amd.so (our own build).
+"""Read the gfx950 code objects inside libkernelforge_hip.so (our own build).
 
 The shared library's ``.hip_fatbin`` section holds one clang offload bundle
 per translation unit. Each bundle is ``__CLANG_OFFLOAD_BUNDLE__`` followed by

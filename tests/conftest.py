@@ -1,6 +1,6 @@
 """Shared pytest configuration.
 
-Markers: ``gpu`` (needs a ROCm device and the built libkernelo_amd.so) and
+Markers: ``gpu`` (needs a ROCm device and the built libkernelforge_hip.so) and
 ``slow``. GPU tests skip on a host without a device, as in the reference
 (tests/conftest.py:7-19); on a GPU host a missing library is a failure, not a
 skip.
@@ -47,6 +47,6 @@ def device():
 
 @pytest.fixture
 def mi355x_caps():
-    from kernelo_amd.runtime.env import MI355X_CAPS
+    from kernelforge.runtime.env import MI355X_CAPS
 
     return MI355X_CAPS

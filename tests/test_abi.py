@@ -1,7 +1,7 @@
 """The C-ABI boundary, without a GPU.
 
-* libkernelo_amd.so loads and exports every function include/kernelo_amd.h
-  declares, and the ctypes binding (kernelo_amd.runtime.hip.SIGNATURES)
+* libkernelforge_hip.so loads and exports every function include/kernelforge_hip.h
+  declares, and the ctypes binding (kernelforge.runtime.hip.SIGNATURES)
   covers exactly that set.
 * Calls that never reach the HIP runtime behave as documented: version and
   target queries, the variant table (which must equal the search space's
@@ -17,10 +17,10 @@ from pathlib import Path
 
 import pytest
 
-from kernelo_amd.runtime import hip
-from kernelo_amd.tuning.search import gemm_instantiations
+from kernelforge.runtime import hip
+from kernelforge.tuning.search import gemm_instantiations
 
-HEADER = Path(__file__).resolve().parent.parent / "include" / "kernelo_amd.h"
+HEADER = Path(__file__).resolve().parent.parent / "include" / "kernelforge_hip.h"
 
 
 def _declared() -> set[str]:

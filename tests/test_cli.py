@@ -10,7 +10,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from kernelo_amd.cli.main import OPERATIONS, build_parser, build_problem, main
+from kernelforge.cli.main import OPERATIONS, build_parser, build_problem, main
 
 
 def parse(argv: list[str]):
@@ -18,7 +18,7 @@ def parse(argv: list[str]):
 
 
 def test_every_operation_is_offered_by_the_cli():
-    from kernelo_amd.kernels import operator_names
+    from kernelforge.kernels import operator_names
 
     assert set(OPERATIONS) == set(operator_names())
 
@@ -27,7 +27,7 @@ def test_version_flag_exits_cleanly(capsys):
     with pytest.raises(SystemExit) as exit_info:
         main(["--version"])
     assert exit_info.value.code == 0
-    assert "kernelo_amd" in capsys.readouterr().out
+    assert "kernelforge" in capsys.readouterr().out
 
 
 def test_missing_subcommand_and_unknown_operation_are_parser_errors():
@@ -92,8 +92,8 @@ def test_report_without_a_database_is_an_error(capsys, tmp_path):
 
 
 def test_cache_list_and_clear(capsys, tmp_path):
-    from kernelo_amd.tuning.cache import ConfigCache
-    from kernelo_amd.tuning.config import KernelConfig, Problem
+    from kernelforge.tuning.cache import ConfigCache
+    from kernelforge.tuning.config import KernelConfig, Problem
 
     path = tmp_path / "configs.json"
     assert main(["cache", "list", "--cache", str(path)]) == 0
@@ -121,4 +121,4 @@ def test_compare_runs_end_to_end(capsys):
                  "--warmup", "5", "--no-db", "--no-cache"])
     assert code == 0
     out = capsys.readouterr().out
-    assert "kernelo_amd" in out and "torch_eager" in out and "GB/s" in out
+    assert "kernelforge" in out and "torch_eager" in out and "GB/s" in out

@@ -2,7 +2,7 @@
 
 The reference asserts on NVIDIA compiler output (tensor-core instructions, one
 exp per epilogue element, shared-memory sizes, no local memory). The same
-intent is checked here on the AMD code objects inside libkernelo_amd.so:
+intent is checked here on the AMD code objects inside libkernelforge_hip.so:
 kernel metadata from ``llvm-readelf --notes`` and instructions from
 ``llvm-objdump -d`` of code this repository compiled.
 """
@@ -14,8 +14,8 @@ import re
 import pytest
 
 from codeobj import load_kernels
-from kernelo_amd.runtime import hip
-from kernelo_amd.tuning.search import (
+from kernelforge.runtime import hip
+from kernelforge.tuning.search import (
     REGISTER_FILE_PER_LANE,
     gemm_direct_lds_bytes,
     gemm_instantiations,

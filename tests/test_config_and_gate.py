@@ -13,15 +13,15 @@ import hashlib
 import pytest
 import torch
 
-from kernelo_amd.dtypes import abi_code, dtype_name, itemsize, parse_dtype
-from kernelo_amd.testing import (
+from kernelforge.dtypes import abi_code, dtype_name, itemsize, parse_dtype
+from kernelforge.testing import (
     ERROR_THRESHOLDS,
     assert_verified,
     exact_fp32_matmul,
     threshold_for,
     verify,
 )
-from kernelo_amd.tuning.config import LAUNCH_KEYS, KernelConfig, Problem
+from kernelforge.tuning.config import LAUNCH_KEYS, KernelConfig, Problem
 
 # --- KernelConfig ----------------------------------------------------------------
 

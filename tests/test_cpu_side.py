@@ -26,27 +26,27 @@ REPO = Path(__file__).resolve().parent.parent
 # --- import hygiene -------------------------------------------------------------------
 
 _MODULES = [
-    "kernelo_amd",
-    "kernelo_amd.dtypes",
-    "kernelo_amd.testing",
-    "kernelo_amd.db",
-    "kernelo_amd.tuning.config",
-    "kernelo_amd.tuning.search",
-    "kernelo_amd.tuning.cache",
-    "kernelo_amd.tuning.tuner",
-    "kernelo_amd.runtime.env",
-    "kernelo_amd.runtime.dispatch",
-    "kernelo_amd.runtime.hip",
-    "kernelo_amd.kernels",
-    "kernelo_amd.kernels.matmul",
-    "kernelo_amd.kernels.fused_linear",
-    "kernelo_amd.kernels.softmax",
-    "kernelo_amd.kernels.rmsnorm",
-    "kernelo_amd.benchmark.runner",
-    "kernelo_amd.benchmark.metrics",
-    "kernelo_amd.benchmark.workloads",
-    "kernelo_amd.profiling",
-    "kernelo_amd.cli.main",
+    "kernelforge",
+    "kernelforge.dtypes",
+    "kernelforge.testing",
+    "kernelforge.db",
+    "kernelforge.tuning.config",
+    "kernelforge.tuning.search",
+    "kernelforge.tuning.cache",
+    "kernelforge.tuning.tuner",
+    "kernelforge.runtime.env",
+    "kernelforge.runtime.dispatch",
+    "kernelforge.runtime.hip",
+    "kernelforge.kernels",
+    "kernelforge.kernels.matmul",
+    "kernelforge.kernels.fused_linear",
+    "kernelforge.kernels.softmax",
+    "kernelforge.kernels.rmsnorm",
+    "kernelforge.benchmark.runner",
+    "kernelforge.benchmark.metrics",
+    "kernelforge.benchmark.workloads",
+    "kernelforge.profiling",
+    "kernelforge.cli.main",
 ]
 
 
@@ -57,8 +57,8 @@ sys.path.insert(0, {str(REPO)!r})
 mods = {_MODULES!r}
 for m in mods:
     __import__(m)
-from kernelo_amd.runtime import hip
-loaded = [l for l in open('/proc/self/maps') if 'libkernelo_amd' in l]
+from kernelforge.runtime import hip
+loaded = [l for l in open('/proc/self/maps') if 'libkernelforge_hip' in l]
 import torch
 print(json.dumps({{"lib_loaded": hip.is_loaded(), "mapped": len(loaded),
                    "cuda_initialized": torch.cuda.is_initialized()}}))
@@ -73,7 +73,7 @@ print(json.dumps({{"lib_loaded": hip.is_loaded(), "mapped": len(loaded),
 
 
 def test_matmul_validation_messages():
-    from kernelo_amd.kernels.matmul import matmul
+    from kernelforge.kernels.matmul import matmul
 
     with pytest.raises(ValueError, match="2D"):
         matmul(torch.ones(2, 2, 2), torch.ones(2, 2))
@@ -86,7 +86,7 @@ def test_matmul_validation_messages():
 
 
 def test_fused_linear_validation_messages():
-    from kernelo_amd.kernels.fused_linear import fused_linear_gelu
+    from kernelforge.kernels.fused_linear import fused_linear_gelu
 
     x, w = torch.ones(2, 3), torch.ones(3, 4)
     with pytest.raises(ValueError, match="2D"):
@@ -100,9 +100,9 @@ def test_fused_linear_validation_messages():
 
 
 def test_row_kernel_validation_messages():
-    from kernelo_amd.kernels.rmsnorm import rmsnorm
-    from kernelo_amd.kernels.softmax import softmax
-    from kernelo_amd.tuning.config import KernelConfig
+    from kernelforge.kernels.rmsnorm import rmsnorm
+    from kernelforge.kernels.softmax import softmax
+    from kernelforge.tuning.config import KernelConfig
 
     with pytest.raises(ValueError, match="2D"):
         softmax(torch.ones(3))
@@ -129,7 +129,7 @@ def test_row_kernel_validation_messages():
 
 
 def test_vector_add_validation_messages():
-    from kernelo_amd.kernels.vector_add import vector_add
+    from kernelforge.kernels.vector_add import vector_add
 
     a = torch.zeros(8, dtype=torch.float16)
     with pytest.raises(ValueError, match="shape mismatch"):
@@ -141,7 +141,7 @@ def test_vector_add_validation_messages():
 
 
 def test_registry_is_lazy_and_named():
-    from kernelo_amd.kernels import get_operator, operator_names
+    from kernelforge.kernels import get_operator, operator_names
 
     assert set(operator_names()) == {"vector_add", "softmax", "matmul", "rmsnorm", "fused_linear"}
     assert get_operator("rmsnorm").name == "rmsnorm"
@@ -151,8 +151,8 @@ def test_registry_is_lazy_and_named():
 
 
 def test_operators_draw_inputs_on_the_cpu_reproducibly():
-    from kernelo_amd.kernels import get_operator
-    from kernelo_amd.tuning.config import Problem
+    from kernelforge.kernels import get_operator
+    from kernelforge.tuning.config import Problem
 
     op = get_operator("fused_linear")
     p = Problem.create("fused_linear", "fp16", M=4, N=8, K=16)
@@ -168,7 +168,7 @@ def test_operators_draw_inputs_on_the_cpu_reproducibly():
 
 
 def _cli(*args: str) -> subprocess.CompletedProcess:
-    return subprocess.run([sys.executable, "-m", "kernelo_amd", *args], capture_output=True,
+    return subprocess.run([sys.executable, "-m", "kernelforge", *args], capture_output=True,
                           text=True, cwd=REPO, timeout=300)
 
 
@@ -181,8 +181,8 @@ def test_cli_explain_and_env_work_without_a_gpu():
 
 
 def test_cli_cache_list_and_clear(tmp_path):
-    from kernelo_amd.tuning.cache import ConfigCache
-    from kernelo_amd.tuning.config import KernelConfig, Problem
+    from kernelforge.tuning.cache import ConfigCache
+    from kernelforge.tuning.config import KernelConfig, Problem
 
     path = tmp_path / "c.json"
     ConfigCache(path).put(Problem.create("matmul", "fp16", M=1, N=2, K=3), "dev", KernelConfig("matmul", A=1))
@@ -200,7 +200,7 @@ def test_cli_errors_exit_nonzero_with_message():
 
 
 def test_cli_parser_defaults():
-    from kernelo_amd.cli.main import build_parser, build_problem
+    from kernelforge.cli.main import build_parser, build_problem
 
     args = build_parser().parse_args(["tune", "rmsnorm"])
     p = build_problem("rmsnorm", args)
@@ -232,7 +232,7 @@ def test_cli_report_without_a_database_exits_2(tmp_path):
 
 
 def test_summarize_agrees_with_numpy():
-    from kernelo_amd.benchmark.runner import summarize
+    from kernelforge.benchmark.runner import summarize
 
     samples = np.random.default_rng(0).gamma(2.0, 0.01, 200)
     r = summarize(samples, warmup=3, iterations=200, timer="hip_event", flushed_l2=True, keep_samples=True)
@@ -247,14 +247,14 @@ def test_summarize_agrees_with_numpy():
 
 
 def test_median_is_robust_to_an_outlier():
-    from kernelo_amd.benchmark.runner import summarize
+    from kernelforge.benchmark.runner import summarize
 
     r = summarize([1.0] * 99 + [1000.0], warmup=0, iterations=100, timer="x", flushed_l2=False)
     assert r.median_ms == 1.0 and r.max_ms == 1000.0
 
 
 def test_cpu_timing_is_labelled_perf_counter():
-    from kernelo_amd.benchmark.runner import benchmark
+    from kernelforge.benchmark.runner import benchmark
 
     r = benchmark(lambda: sum(range(100)), warmup=1, iterations=5, device="cpu")
     assert r.timer == "perf_counter" and not r.flushed_l2 and r.iterations == 5
@@ -263,7 +263,7 @@ def test_cpu_timing_is_labelled_perf_counter():
 
 
 def test_metrics():
-    from kernelo_amd.benchmark import metrics
+    from kernelforge.benchmark import metrics
 
     assert metrics.matmul_flops(2048, 4096, 4096) == 68719476736
     assert metrics.rmsnorm_bytes(4096, 4096, 4) == 134234112

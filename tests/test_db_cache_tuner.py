@@ -17,14 +17,14 @@ from collections.abc import Iterator
 import pytest
 import torch
 
-from kernelo_amd.db import SCHEMA_VERSION, Measurement, ResultsDB
-from kernelo_amd.kernels.base import Operator
-from kernelo_amd.runtime.dispatch import select_config
-from kernelo_amd.runtime.env import MI355X_CAPS, capture_environment
-from kernelo_amd.tuning.cache import CACHE_VERSION, ConfigCache
-from kernelo_amd.tuning.config import KernelConfig, Problem
-from kernelo_amd.tuning.search import SearchSpace
-from kernelo_amd.tuning.tuner import (
+from kernelforge.db import SCHEMA_VERSION, Measurement, ResultsDB
+from kernelforge.kernels.base import Operator
+from kernelforge.runtime.dispatch import select_config
+from kernelforge.runtime.env import MI355X_CAPS, capture_environment
+from kernelforge.tuning.cache import CACHE_VERSION, ConfigCache
+from kernelforge.tuning.config import KernelConfig, Problem
+from kernelforge.tuning.search import SearchSpace
+from kernelforge.tuning.tuner import (
     STATUS_COMPILE_ERROR,
     STATUS_INCORRECT,
     STATUS_OK,
@@ -48,14 +48,14 @@ def test_db_round_trip_and_dedup(tmp_path):
     run = db.start_run(env, notes="t", version="x")
     cfg = KernelConfig("fake", MODE=0)
     db.record_many(run, _problem(), [
-        Measurement(label="kernelo_amd", status=STATUS_OK, config=cfg, tflops=1.0),
-        Measurement(label="kernelo_amd", status=STATUS_INCORRECT, config=cfg, error="bad"),
+        Measurement(label="kernelforge", status=STATUS_OK, config=cfg, tflops=1.0),
+        Measurement(label="kernelforge", status=STATUS_INCORRECT, config=cfg, error="bad"),
         Measurement(label="torch_eager", status=STATUS_OK),
     ])
     counts = db.counts()
     assert counts == {"runs": 1, "problems": 1, "configs": 1, "results": 3}
     rows = db.rows(operation="fake")
-    assert [r["label"] for r in rows] == ["kernelo_amd", "kernelo_amd", "torch_eager"]
+    assert [r["label"] for r in rows] == ["kernelforge", "kernelforge", "torch_eager"]
     assert rows[0]["digest"] == cfg.digest and rows[2]["params_json"] is None
     assert db.operations() == ["fake"]
     assert len(db.runs()) == 1
@@ -76,8 +76,8 @@ def test_db_schema_version_is_checked(tmp_path):
 
 
 def test_best_per_label_ignores_incorrect_rows(tmp_path):
-    from kernelo_amd.benchmark.runner import summarize
-    from kernelo_amd.testing import verify
+    from kernelforge.benchmark.runner import summarize
+    from kernelforge.testing import verify
 
     db = ResultsDB(":memory:")
     run = db.start_run(capture_environment())
@@ -85,8 +85,8 @@ def test_best_per_label_ignores_incorrect_rows(tmp_path):
     bad = verify(torch.ones(2), torch.zeros(2))
     t = lambda ms: summarize([ms], warmup=0, iterations=1, timer="perf_counter", flushed_l2=False)
     db.record_many(run, _problem(), [
-        Measurement("kernelo_amd", STATUS_OK, KernelConfig("fake", MODE=0), good, t(2.0)),
-        Measurement("kernelo_amd", STATUS_INCORRECT, KernelConfig("fake", MODE=1), bad, t(1.0)),
+        Measurement("kernelforge", STATUS_OK, KernelConfig("fake", MODE=0), good, t(2.0)),
+        Measurement("kernelforge", STATUS_INCORRECT, KernelConfig("fake", MODE=1), bad, t(1.0)),
     ])
     (best,) = db.best_per_label()
     assert best["median_us"] == pytest.approx(2000.0)
@@ -131,7 +131,7 @@ def test_cache_write_is_atomic(tmp_path):
 
 
 def test_packaged_winners_file_is_valid_and_keyed_for_mi355x():
-    from kernelo_amd.tuning.cache import PACKAGED_CACHE
+    from kernelforge.tuning.cache import PACKAGED_CACHE
 
     cache = ConfigCache(PACKAGED_CACHE)
     keys = {e.device_key for e in cache.entries()}
@@ -141,7 +141,7 @@ def test_packaged_winners_file_is_valid_and_keyed_for_mi355x():
 
 
 def test_dispatch_hit_packaged_and_default(tmp_path):
-    from kernelo_amd.kernels import get_operator
+    from kernelforge.kernels import get_operator
 
     op = get_operator("matmul")
     problem = Problem.create("matmul", "fp16", M=64, N=64, K=64)
@@ -277,7 +277,7 @@ def test_classify(exc, status):
 
 
 def test_hip_error_classes_classify_as_the_tuner_expects():
-    from kernelo_amd.runtime import hip
+    from kernelforge.runtime import hip
 
     assert _classify(hip.KernelNotCompiled("x"))[0] == STATUS_COMPILE_ERROR
     assert _classify(hip.KernelOutOfResources("x"))[0] == STATUS_COMPILE_ERROR

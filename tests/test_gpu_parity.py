@@ -13,10 +13,10 @@ from __future__ import annotations
 import pytest
 import torch
 
-from kernelo_amd.benchmark.workloads import MATMUL_SHAPES, ROW_SHAPES
-from kernelo_amd.runtime import hip
-from kernelo_amd.testing import verify
-from kernelo_amd.tuning.config import KernelConfig
+from kernelforge.benchmark.workloads import MATMUL_SHAPES, ROW_SHAPES
+from kernelforge.runtime import hip
+from kernelforge.testing import verify
+from kernelforge.tuning.config import KernelConfig
 from oracle import ops
 
 pytestmark = pytest.mark.gpu
@@ -41,7 +41,7 @@ def _gate(ref: torch.Tensor, out: torch.Tensor, dtype: torch.dtype, what: str) -
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
 @pytest.mark.parametrize("rows,cols", ROW_SHAPES["correctness"])
 def test_rmsnorm_correctness_suite(rows, cols, dtype):
-    from kernelo_amd.kernels.rmsnorm import rmsnorm
+    from kernelforge.kernels.rmsnorm import rmsnorm
 
     x = _randn(rows, cols, dtype=dtype, seed=rows * 7 + cols)
     g = (_randn(cols, dtype=torch.float32, seed=cols) * 0.1 + 1.0).to(dtype)
@@ -53,7 +53,7 @@ def test_rmsnorm_correctness_suite(rows, cols, dtype):
 @pytest.mark.parametrize("rpp", (1, 2, 4, 8))
 def test_rmsnorm_configs(warps, rpp):
     """Every wave count and rows-per-program, including tails of the row loop."""
-    from kernelo_amd.kernels.rmsnorm import rmsnorm
+    from kernelforge.kernels.rmsnorm import rmsnorm
 
     rows, cols = 333, 4096
     x = _randn(rows, cols, dtype=torch.float16, seed=3)
@@ -65,7 +65,7 @@ def test_rmsnorm_configs(warps, rpp):
 
 def test_rmsnorm_baseline_config_fp32():
     """x[4096,4096] ~ N(0,1), gamma ~ N(1, 0.1), eps=1e-6, fp32."""
-    from kernelo_amd.kernels.rmsnorm import rmsnorm
+    from kernelforge.kernels.rmsnorm import rmsnorm
 
     g0 = torch.Generator().manual_seed(0)
     x = torch.randn(4096, 4096, generator=g0)
@@ -75,7 +75,7 @@ def test_rmsnorm_baseline_config_fp32():
 
 
 def test_rmsnorm_zero_row_is_zero_and_finite():
-    from kernelo_amd.kernels.rmsnorm import rmsnorm
+    from kernelforge.kernels.rmsnorm import rmsnorm
 
     x = torch.zeros(4, 1024, dtype=torch.float16, device=DEV)
     g = torch.ones(1024, dtype=torch.float16, device=DEV)
@@ -89,7 +89,7 @@ def test_rmsnorm_zero_row_is_zero_and_finite():
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
 @pytest.mark.parametrize("rows,cols", ROW_SHAPES["correctness"])
 def test_softmax_correctness_suite(rows, cols, dtype):
-    from kernelo_amd.kernels.softmax import softmax
+    from kernelforge.kernels.softmax import softmax
 
     x = _randn(rows, cols, dtype=dtype, seed=rows * 13 + cols, scale=3.0)
     out = softmax(x.to(DEV))
@@ -99,7 +99,7 @@ def test_softmax_correctness_suite(rows, cols, dtype):
 @pytest.mark.parametrize("cols", (4096, 11008))
 def test_softmax_overflow_rows(cols):
     """BASELINE config 2 recipe at 512 rows: N(0,3), 1% of rows shifted by +60, fp16."""
-    from kernelo_amd.kernels.softmax import softmax
+    from kernelforge.kernels.softmax import softmax
 
     rows = 512
     g = torch.Generator().manual_seed(0)
@@ -115,7 +115,7 @@ def test_softmax_overflow_rows(cols):
 
 
 def test_softmax_constant_row_is_exactly_one_over_n():
-    from kernelo_amd.kernels.softmax import softmax
+    from kernelforge.kernels.softmax import softmax
 
     x = torch.full((3, 4096), 7.25, dtype=torch.float16, device=DEV)
     out = softmax(x)
@@ -125,7 +125,7 @@ def test_softmax_constant_row_is_exactly_one_over_n():
 @pytest.mark.parametrize("warps", (1, 4, 16))
 @pytest.mark.parametrize("rpp", (1, 3, 8))
 def test_softmax_configs(warps, rpp):
-    from kernelo_amd.kernels.softmax import softmax
+    from kernelforge.kernels.softmax import softmax
 
     rows, cols = 77, 2000
     x = _randn(rows, cols, dtype=torch.bfloat16, seed=5, scale=3.0)
@@ -142,7 +142,7 @@ _GEMM_SHAPES = [s for s in MATMUL_SHAPES["correctness"] if s[0] * s[1] * s[2] <=
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
 @pytest.mark.parametrize("m,n,k", _GEMM_SHAPES)
 def test_matmul_correctness_suite(m, n, k, dtype):
-    from kernelo_amd.kernels.matmul import matmul
+    from kernelforge.kernels.matmul import matmul
 
     a = _randn(m, k, dtype=dtype, seed=m + 3 * n + 7 * k)
     b = _randn(k, n, dtype=dtype, seed=m * n + k)
@@ -183,7 +183,7 @@ def test_matmul_tiles_and_layouts(tile, layout, m, n, k, dtype):
     """Every loader pair and pipeline: row-major B (VecN / DMA + transposing
     reads), transposed B (VecK / DMA), strided A (scalar); K tails that are and
     are not multiples of 8 (the DMA path zeroes chunks past K)."""
-    from kernelo_amd.kernels.matmul import matmul
+    from kernelforge.kernels.matmul import matmul
 
     bm, bn, bk, w, direct, stages = tile
     a = _randn(m, k, dtype=dtype, seed=1)
@@ -204,7 +204,7 @@ def test_matmul_tiles_and_layouts(tile, layout, m, n, k, dtype):
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16), ids=("fp16", "bf16"))
 def test_matmul_baseline_config(dtype):
     """BASELINE config 3 (fp16) and its bf16 twin: A[2048,4096] @ B[4096,4096], N(0,1)/sqrt(K)."""
-    from kernelo_amd.kernels.matmul import matmul
+    from kernelforge.kernels.matmul import matmul
 
     a = _randn(2048, 4096, dtype=dtype, seed=0, scale=4096**-0.5)
     b = _randn(4096, 4096, dtype=dtype, seed=1, scale=4096**-0.5)
@@ -215,7 +215,7 @@ def test_matmul_baseline_config(dtype):
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
 @pytest.mark.parametrize("m,n,k", [(1, 7, 3), (127, 127, 127), (257, 129, 65), (511, 769, 1025)])
 def test_fused_linear_correctness(m, n, k, dtype):
-    from kernelo_amd.kernels.fused_linear import fused_linear_gelu
+    from kernelforge.kernels.fused_linear import fused_linear_gelu
 
     x = _randn(m, k, dtype=dtype, seed=m + k)
     w = _randn(k, n, dtype=dtype, seed=n, scale=k**-0.5)
@@ -225,8 +225,8 @@ def test_fused_linear_correctness(m, n, k, dtype):
 
 
 def test_staged_tile_that_was_not_built_is_reported():
-    from kernelo_amd.kernels.matmul import matmul
-    from kernelo_amd.runtime import hip
+    from kernelforge.kernels.matmul import matmul
+    from kernelforge.runtime import hip
 
     a = torch.ones(64, 64, dtype=torch.float16, device=DEV)
     cfg = KernelConfig("matmul", BLOCK_M=256, BLOCK_N=256, BLOCK_K=64, GROUP_M=8, DIRECT=0,
@@ -237,7 +237,7 @@ def test_staged_tile_that_was_not_built_is_reported():
 
 def test_fused_linear_transposed_weight():
     """nn.Linear stores weight as (N, K); the kernel reads weight.t() through strides."""
-    from kernelo_amd.kernels.fused_linear import fused_linear_gelu
+    from kernelforge.kernels.fused_linear import fused_linear_gelu
 
     m, n, k = 300, 520, 256
     x = _randn(m, k, dtype=torch.float16, seed=1)
@@ -249,7 +249,7 @@ def test_fused_linear_transposed_weight():
 
 def test_fused_linear_identity_weight_traces_gelu():
     """Identity weight, zero bias: the output is gelu_tanh(x) over [-60, 60] and +-1e4."""
-    from kernelo_amd.kernels.fused_linear import fused_linear_gelu
+    from kernelforge.kernels.fused_linear import fused_linear_gelu
 
     n = 128
     vals = torch.cat([torch.linspace(-60, 60, 126), torch.tensor([-1e4, 1e4])])
@@ -263,7 +263,7 @@ def test_fused_linear_identity_weight_traces_gelu():
 
 
 def test_fused_linear_zero_weight_is_gelu_of_bias():
-    from kernelo_amd.kernels.fused_linear import fused_linear_gelu
+    from kernelforge.kernels.fused_linear import fused_linear_gelu
 
     m, n, k = 64, 256, 64
     x = _randn(m, k, dtype=torch.float16, seed=1)
@@ -279,7 +279,7 @@ def test_fused_linear_zero_weight_is_gelu_of_bias():
 
 def test_gemv_single_row_caps_the_workgroup_at_eight_waves():
     """One x row keeps 16 rows of W in flight per lane: 512 lanes at most."""
-    from kernelo_amd.kernels.matmul import matmul
+    from kernelforge.kernels.matmul import matmul
 
     x = torch.ones(1, 256, dtype=torch.bfloat16, device=DEV)
     w = torch.ones(256, 512, dtype=torch.bfloat16, device=DEV)
@@ -293,7 +293,7 @@ def test_gemv_single_row_caps_the_workgroup_at_eight_waves():
 @pytest.mark.parametrize("lanes", (8, 16, 32, 64))
 def test_gemv_decode_config(split, warps, lanes):
     """BASELINE config 5a: bf16 1x11008x4096, U(-1, 1), every strip width."""
-    from kernelo_amd.kernels.matmul import matmul
+    from kernelforge.kernels.matmul import matmul
 
     g = torch.Generator().manual_seed(0)
     x = (torch.rand(1, 4096, generator=g) * 2 - 1).to(torch.bfloat16)
@@ -311,7 +311,7 @@ def test_gemv_x_layouts(layout, m, dtype, k, split):
     """x rows loaded as one vector per trip (k-contiguous, aligned slice starts)
     or element by element (strided or misaligned x, slices starting off a
     multiple of the trip's rows), plus the rows after the last whole trip."""
-    from kernelo_amd.kernels.matmul import matmul
+    from kernelforge.kernels.matmul import matmul
 
     x = _randn(m, k, dtype=dtype, seed=k + m)
     w = _randn(k, 2056, dtype=dtype, seed=7, scale=k**-0.5)
@@ -329,7 +329,7 @@ def test_gemv_x_layouts(layout, m, dtype, k, split):
 
 
 def test_gemv_is_deterministic():
-    from kernelo_amd.kernels.matmul import matmul
+    from kernelforge.kernels.matmul import matmul
 
     x = _randn(1, 4096, dtype=torch.bfloat16, seed=1).to(DEV)
     w = _randn(4096, 11008, dtype=torch.bfloat16, seed=2).to(DEV)
@@ -343,7 +343,7 @@ def test_gemv_is_deterministic():
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
 @pytest.mark.parametrize("lanes", (8, 16, 64))
 def test_gemv_small_batches(m, dtype, lanes):
-    from kernelo_amd.kernels.matmul import matmul
+    from kernelforge.kernels.matmul import matmul
 
     x = _randn(m, 1000, dtype=dtype, seed=m)
     w = _randn(1000, 3000, dtype=dtype, seed=9, scale=1000**-0.5)
@@ -360,7 +360,7 @@ def test_gemv_small_batches(m, dtype, lanes):
 @pytest.mark.parametrize("lanes", (8, 16, 32, 64))
 def test_gemv_k_contiguous_weight(split, warps, lanes):
     """x @ weight.t() with weight [N, K] row-major: the dot layout."""
-    from kernelo_amd.kernels.matmul import matmul
+    from kernelforge.kernels.matmul import matmul
 
     g = torch.Generator().manual_seed(1)
     x = (torch.rand(1, 4096, generator=g) * 2 - 1).to(torch.bfloat16)
@@ -375,8 +375,8 @@ def test_gemv_k_contiguous_weight(split, warps, lanes):
 @pytest.mark.parametrize("k", (1000, 1004, 8, 0))
 def test_gemv_k_contiguous_batches_and_odd_k(m, dtype, k):
     """Rows of x, every dtype; K % 8 != 0 (1004 fp16) takes the general path."""
-    from kernelo_amd.kernels.fused_linear import fused_linear_gelu
-    from kernelo_amd.kernels.matmul import matmul
+    from kernelforge.kernels.fused_linear import fused_linear_gelu
+    from kernelforge.kernels.matmul import matmul
 
     x = _randn(m, k, dtype=dtype, seed=m + k)
     weight = _randn(777, k, dtype=dtype, seed=3, scale=max(k, 1) ** -0.5)
@@ -390,7 +390,7 @@ def test_gemv_k_contiguous_batches_and_odd_k(m, dtype, k):
 
 
 def test_gemv_k_contiguous_is_deterministic_and_matches_the_strip_kernel():
-    from kernelo_amd.kernels.matmul import matmul
+    from kernelforge.kernels.matmul import matmul
 
     x = _randn(1, 4096, dtype=torch.float16, seed=5).to(DEV)
     weight = _randn(11008, 4096, dtype=torch.float16, seed=6, scale=1 / 64).to(DEV)
@@ -410,8 +410,8 @@ def _guarded_call(m, n, k, cfg, seed, dtype=torch.bfloat16):
     8 guard rows above and below); return (inside, guard_intact)."""
     import ctypes
 
-    from kernelo_amd.dtypes import abi_code
-    from kernelo_amd.runtime import hip
+    from kernelforge.dtypes import abi_code
+    from kernelforge.runtime import hip
 
     g = torch.Generator().manual_seed(seed)
     a = (torch.rand(m, k, generator=g) * 2 - 1).to(dtype)
@@ -480,10 +480,10 @@ def test_graph_replays_match_eager_results():
     three replays, with eager work and synchronisations in between, each
     bitwise equal to the eager results. The split-K GEMV's ticket counters are
     reset by the kernel itself, so replays need no memset node."""
-    from kernelo_amd.kernels.fused_linear import fused_linear_gelu
-    from kernelo_amd.kernels.matmul import matmul
-    from kernelo_amd.kernels.rmsnorm import rmsnorm
-    from kernelo_amd.kernels.softmax import softmax
+    from kernelforge.kernels.fused_linear import fused_linear_gelu
+    from kernelforge.kernels.matmul import matmul
+    from kernelforge.kernels.rmsnorm import rmsnorm
+    from kernelforge.kernels.softmax import softmax
 
     a = _randn(300, 520, dtype=torch.float16, seed=1).to(DEV)
     b = _randn(520, 264, dtype=torch.float16, seed=2).to(DEV)

@@ -14,10 +14,10 @@ from __future__ import annotations
 import pytest
 import torch
 
-from kernelo_amd.dtypes import abi_code
-from kernelo_amd.runtime import hip
-from kernelo_amd.testing import verify
-from kernelo_amd.tuning.config import KernelConfig
+from kernelforge.dtypes import abi_code
+from kernelforge.runtime import hip
+from kernelforge.testing import verify
+from kernelforge.tuning.config import KernelConfig
 from oracle import ops
 
 pytestmark = pytest.mark.gpu
@@ -129,7 +129,7 @@ def test_shared_workspace_serves_any_sequence_of_calls():
     partial sums written by one call never sit where a later call, with more
     blocks, expects a zero counter. The sequence grows the counter count after
     a call with large partials, the order that exposes an overlap."""
-    from kernelo_amd.kernels.matmul import launch_gemm
+    from kernelforge.kernels.matmul import launch_gemm
 
     cases = [
         # (m, n, k, config)
@@ -200,7 +200,7 @@ def test_concurrent_tiles_on_mi355x():
 def test_split_k_with_only_full_rounds_runs_unsplit():
     """256 tiles of 256x128 fill exactly one round: nothing is split, so the
     result is bitwise the unsplit kernel's."""
-    from kernelo_amd.kernels.matmul import matmul
+    from kernelforge.kernels.matmul import matmul
 
     a = _randn(2048, 1024, dtype=torch.float16, seed=30).to(DEV)
     b = _randn(1024, 4096, dtype=torch.float16, seed=31, scale=1 / 32).to(DEV)
@@ -225,8 +225,8 @@ def test_split_k_on_a_layout_the_dma_cannot_take_runs_unsplit():
 def test_split_k_through_the_operator_and_a_graph():
     """matmul() with a SPLIT_K config, eager and as HIP graph replays (the
     kernel returns its counters to zero, so replays need no memset node)."""
-    from kernelo_amd.kernels.fused_linear import fused_linear_gelu
-    from kernelo_amd.kernels.matmul import matmul
+    from kernelforge.kernels.fused_linear import fused_linear_gelu
+    from kernelforge.kernels.matmul import matmul
 
     cfg = KernelConfig("matmul", BLOCK_M=32, BLOCK_N=64, BLOCK_K=64, GROUP_M=8, DIRECT=1,
                        SPLIT_K=4, num_warps=4, num_stages=3)

@@ -20,12 +20,12 @@ import sys
 import pytest
 import torch
 
-from kernelo_amd.benchmark.workloads import VECTOR_SHAPES
-from kernelo_amd.dtypes import abi_code
-from kernelo_amd.runtime import hip
-from kernelo_amd.testing import verify
-from kernelo_amd.tuning.config import KernelConfig, Problem
-from kernelo_amd.tuning.search import TWO_PASS_MAX_STAGED_BYTES, two_pass_block
+from kernelforge.benchmark.workloads import VECTOR_SHAPES
+from kernelforge.dtypes import abi_code
+from kernelforge.runtime import hip
+from kernelforge.testing import verify
+from kernelforge.tuning.config import KernelConfig, Problem
+from kernelforge.tuning.search import TWO_PASS_MAX_STAGED_BYTES, two_pass_block
 from oracle import ops
 
 pytestmark = pytest.mark.gpu
@@ -55,7 +55,7 @@ def _gate(ref: torch.Tensor, out: torch.Tensor, dtype: torch.dtype, what: str) -
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
 @pytest.mark.parametrize("n", VECTOR_SHAPES["correctness"])
 def test_vector_add_is_bit_exact_across_sizes(n, dtype):
-    from kernelo_amd.kernels.vector_add import DEFAULT_CONFIG, vector_add
+    from kernelforge.kernels.vector_add import DEFAULT_CONFIG, vector_add
 
     a = _randn(n, dtype=dtype, seed=n)
     b = _randn(n, dtype=dtype, seed=n + 1)
@@ -65,9 +65,9 @@ def test_vector_add_is_bit_exact_across_sizes(n, dtype):
 
 
 def test_vector_add_every_candidate_agrees():
-    from kernelo_amd.kernels.vector_add import vector_add
-    from kernelo_amd.runtime.env import MI355X_CAPS
-    from kernelo_amd.tuning.search import VectorAddSearchSpace
+    from kernelforge.kernels.vector_add import vector_add
+    from kernelforge.runtime.env import MI355X_CAPS
+    from kernelforge.tuning.search import VectorAddSearchSpace
 
     n = 1_000_003
     a = _randn(n, dtype=torch.float16, seed=5)
@@ -85,7 +85,7 @@ def test_vector_add_every_candidate_agrees():
 def test_vector_add_unaligned_and_strided_operands(dtype):
     """Views that start off a 16-byte boundary take the element path; a
     strided view is made contiguous by the wrapper, as in the reference."""
-    from kernelo_amd.kernels.vector_add import vector_add
+    from kernelforge.kernels.vector_add import vector_add
 
     n = 70_001
     big_a = _randn(n + 3, dtype=dtype, seed=7)
@@ -113,7 +113,7 @@ def test_vector_add_writes_nothing_past_n():
 
 
 def test_vector_add_validates_device_inputs():
-    from kernelo_amd.kernels.vector_add import vector_add
+    from kernelforge.kernels.vector_add import vector_add
 
     a = torch.zeros(8, device=DEV, dtype=torch.float16)
     with pytest.raises(ValueError, match="shape mismatch"):
@@ -131,7 +131,7 @@ WIDE_SHAPES = [(3, 16385), (5, 40000), (2, 65536), (4, 100003), (7, 1), (3, 127)
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
 @pytest.mark.parametrize("rows,cols", WIDE_SHAPES)
 def test_two_pass_rmsnorm_default_and_both_stagings(rows, cols, dtype):
-    from kernelo_amd.kernels.rmsnorm import rmsnorm
+    from kernelforge.kernels.rmsnorm import rmsnorm
 
     x = _randn(rows, cols, dtype=dtype, seed=rows * 13 + cols, scale=2.0)
     g = (_randn(cols, dtype=torch.float32, seed=cols) * 0.1 + 1.0).to(dtype)
@@ -153,7 +153,7 @@ def test_two_pass_rmsnorm_default_and_both_stagings(rows, cols, dtype):
 @pytest.mark.parametrize("stage", (0, 1))
 def test_two_pass_rmsnorm_trip_shapes(warps, unroll, rpp, stage):
     """Every unroll and wave count, rows-per-program tails, staged or not."""
-    from kernelo_amd.kernels.rmsnorm import rmsnorm
+    from kernelforge.kernels.rmsnorm import rmsnorm
 
     rows, cols = 37, 20000
     x = _randn(rows, cols, dtype=torch.float16, seed=21)
@@ -165,9 +165,9 @@ def test_two_pass_rmsnorm_trip_shapes(warps, unroll, rpp, stage):
 
 
 def test_two_pass_rmsnorm_every_candidate_agrees():
-    from kernelo_amd.kernels.rmsnorm import rmsnorm
-    from kernelo_amd.runtime.env import MI355X_CAPS
-    from kernelo_amd.tuning.search import RMSNormSearchSpace
+    from kernelforge.kernels.rmsnorm import rmsnorm
+    from kernelforge.runtime.env import MI355X_CAPS
+    from kernelforge.tuning.search import RMSNormSearchSpace
 
     rows, cols = 64, 24000
     x = _randn(rows, cols, dtype=torch.bfloat16, seed=23)
@@ -208,7 +208,7 @@ def test_two_pass_rmsnorm_unaligned_strided_rows_and_guard_band(stage):
 
 
 def test_two_pass_rmsnorm_matches_single_pass_where_both_fit():
-    from kernelo_amd.kernels.rmsnorm import default_config, rmsnorm
+    from kernelforge.kernels.rmsnorm import default_config, rmsnorm
 
     x = _randn(256, 8192, dtype=torch.float32, seed=27).to(DEV)
     g = (_randn(8192, dtype=torch.float32, seed=28) * 0.1 + 1.0).to(DEV)
@@ -220,7 +220,7 @@ def test_two_pass_rmsnorm_matches_single_pass_where_both_fit():
 
 
 def test_two_pass_rmsnorm_zero_row_and_zero_size():
-    from kernelo_amd.kernels.rmsnorm import rmsnorm
+    from kernelforge.kernels.rmsnorm import rmsnorm
 
     x = torch.zeros(3, 30000, dtype=torch.float16, device=DEV)
     g = torch.ones(30000, dtype=torch.float16, device=DEV)
@@ -234,7 +234,7 @@ def test_wide_row_full_size_is_deterministic_and_normalised():
     oracle run over every row: two runs are bitwise equal, every row's
     mean square after dividing out gamma is 1, and a sample of rows passes
     the gate against the oracle."""
-    from kernelo_amd.kernels.rmsnorm import rmsnorm
+    from kernelforge.kernels.rmsnorm import rmsnorm
 
     rows, cols = 4096, 32768
     x = _randn(rows, cols, dtype=torch.float16, seed=29).to(DEV)
@@ -252,7 +252,7 @@ def test_wide_row_full_size_is_deterministic_and_normalised():
 
 
 def _block(seed=0):
-    from kernelo_amd.integration.transformer import BlockConfig, TransformerBlock
+    from kernelforge.integration.transformer import BlockConfig, TransformerBlock
 
     torch.manual_seed(seed)
     block = TransformerBlock(BlockConfig(hidden=256, heads=8, intermediate=512), device=DEV,
@@ -267,7 +267,7 @@ def _block(seed=0):
 
 @pytest.mark.parametrize("batch,seq", [(2, 128), (1, 1), (1, 7), (3, 5)])
 def test_block_backends_agree_on_one_set_of_weights(batch, seq):
-    from kernelo_amd.integration.transformer import BACKEND_KERNELO, BACKEND_TORCH
+    from kernelforge.integration.transformer import BACKEND_KERNELO, BACKEND_TORCH
 
     block = _block()
     x = _randn(batch, seq, 256, dtype=torch.float16, seed=31).to(DEV)
@@ -281,7 +281,7 @@ def test_block_backends_agree_on_one_set_of_weights(batch, seq):
 
 
 def test_block_resolves_configurations_once_per_shape():
-    from kernelo_amd.integration.transformer import BACKEND_KERNELO
+    from kernelforge.integration.transformer import BACKEND_KERNELO
 
     block = _block()
     block.backend = BACKEND_KERNELO
@@ -303,7 +303,7 @@ def test_block_validates_its_input():
 
 
 def test_benchmark_block_times_both_backends():
-    from kernelo_amd.integration.transformer import BACKENDS, BlockConfig, benchmark_block
+    from kernelforge.integration.transformer import BACKENDS, BlockConfig, benchmark_block
 
     results = benchmark_block(BlockConfig(hidden=256, heads=8, intermediate=512), batch=1, seq=128,
                               device=DEV, warmup=2, iterations=5)
@@ -316,7 +316,7 @@ def test_benchmark_block_times_both_backends():
 
 
 def _cli(*argv, timeout=240):
-    return subprocess.run([sys.executable, "-m", "kernelo_amd", *argv], capture_output=True,
+    return subprocess.run([sys.executable, "-m", "kernelforge", *argv], capture_output=True,
                           text=True, timeout=timeout)
 
 
@@ -326,7 +326,7 @@ def test_cli_benchmark_then_report(tmp_path):
         run = _cli("benchmark", op, "--suite", "smoke", "--dtype", "fp16", "--db", str(db),
                    "--no-cache", "--warmup", "3", "--iterations", "10")
         assert run.returncode == 0, run.stdout + run.stderr
-        assert "kernelo_amd" in run.stdout and "GB/s" in run.stdout
+        assert "kernelforge" in run.stdout and "GB/s" in run.stdout
     rep = _cli("report", "--db", str(db), "--out", str(out))
     assert rep.returncode == 0, rep.stderr
     text = (out / "summary.md").read_text()
@@ -338,8 +338,8 @@ def test_cli_compare_one_shape_and_a_block(tmp_path):
     run = _cli("compare", "rmsnorm", "--rows", "64", "--cols", "20000", "--dtype", "fp32",
                "--no-cache", "--warmup", "2", "--iterations", "5")
     assert run.returncode == 0, run.stdout + run.stderr
-    assert "kernelo_amd" in run.stdout and "torch_eager" in run.stdout
+    assert "kernelforge" in run.stdout and "torch_eager" in run.stdout
     run = _cli("compare", "transformer", "--hidden", "256", "--heads", "8", "--intermediate", "512",
                "--seq", "64", "--no-cache", "--warmup", "2", "--iterations", "5")
     assert run.returncode == 0, run.stdout + run.stderr
-    assert "Block latency" in run.stdout and "kernelo_amd" in run.stdout
+    assert "Block latency" in run.stdout and "kernelforge" in run.stdout

@@ -1,5 +1,5 @@
 """TransformerBlock without a GPU: geometry checks, backend selection, a
-closed form of the torch backend, and that the kernelo_amd backend refuses
+closed form of the torch backend, and that the kernelforge backend refuses
 host tensors instead of falling back (kernelforge/tests/test_transformer.py:
 25-34). The backend-parity tests run on the GPU (test_gpu_widening.py).
 """
@@ -9,7 +9,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from kernelo_amd.integration.transformer import (
+from kernelforge.integration.transformer import (
     BACKEND_KERNELO,
     BACKEND_TORCH,
     BACKENDS,

@@ -23,7 +23,7 @@ import numpy as np
 import pytest
 import torch
 
-from kernelo_amd.testing import verify
+from kernelforge.testing import verify
 from oracle import ops
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "kernels_fp64.npz"

@@ -11,12 +11,12 @@ from __future__ import annotations
 
 import pytest
 
-from kernelo_amd.benchmark import report
-from kernelo_amd.benchmark.runner import summarize
-from kernelo_amd.db import Measurement, ResultsDB
-from kernelo_amd.runtime.env import capture_environment
-from kernelo_amd.testing import VerificationResult
-from kernelo_amd.tuning.config import KernelConfig, Problem
+from kernelforge.benchmark import report
+from kernelforge.benchmark.runner import summarize
+from kernelforge.db import Measurement, ResultsDB
+from kernelforge.runtime.env import capture_environment
+from kernelforge.testing import VerificationResult
+from kernelforge.tuning.config import KernelConfig, Problem
 
 pytest.importorskip("pandas")
 pytest.importorskip("matplotlib")
@@ -45,18 +45,18 @@ def seeded(tmp_path):
         problem = Problem.create("matmul", "fp16", M=m, N=n, K=k)
         flops = 2 * m * n * k
         for label, ms, cfg in (("torch_eager", eager, None), ("hip_default", mine * 1.3, _tile(128, 128)),
-                               ("kernelo_amd", mine, _tile(128, 256))):
+                               ("kernelforge", mine, _tile(128, 256))):
             db.record(run, problem, Measurement(label=label, status="ok", config=cfg,
                                                 verification=_ok(), timing=_timing(ms),
                                                 tflops=flops / (ms * 1e-3) / 1e12))
         for (bm, bn), factor in (((64, 64), 1.9), ((128, 128), 1.2), ((256, 128), 1.05)):
             ms = mine * factor
-            db.record(run, problem, Measurement(label="kernelo_amd", status="ok", config=_tile(bm, bn),
+            db.record(run, problem, Measurement(label="kernelforge", status="ok", config=_tile(bm, bn),
                                                 verification=_ok(), timing=_timing(ms),
                                                 tflops=flops / (ms * 1e-3) / 1e12))
     rms = Problem.create("rmsnorm", "fp32", rows=4096, cols=4096)
     moved = (2 * 4096 * 4096 + 4096) * 4
-    for label, ms in (("torch_eager", 0.061), ("kernelo_amd", 0.0266)):
+    for label, ms in (("torch_eager", 0.061), ("kernelforge", 0.0266)):
         db.record(run, rms, Measurement(label=label, status="ok", verification=_ok(),
                                         timing=_timing(ms), gbps=moved / (ms * 1e-3) / 1e9))
     yield db
@@ -93,7 +93,7 @@ def test_fastest_row_per_label_is_reported(seeded, tmp_path):
     report.generate(seeded, tmp_path / "out")
     with open(tmp_path / "out" / "matmul.csv") as fh:
         rows = list(csv.DictReader(fh))
-    tuned = [r for r in rows if r["label"] == "kernelo_amd"]
+    tuned = [r for r in rows if r["label"] == "kernelforge"]
     assert len(tuned) == 2  # one per shape, the fastest of four candidates
     assert sorted(round(float(r["median_us"]), 1) for r in tuned) == [24.0, 69.0]
 
@@ -103,7 +103,7 @@ def test_two_dtypes_at_one_shape_are_two_series(tmp_path):
         run = db.start_run(capture_environment())
         for dtype, ms in (("fp16", 1.0), ("bf16", 1.1)):
             p = Problem.create("matmul", dtype, M=512, N=512, K=512)
-            for label, v in (("torch_eager", ms), ("kernelo_amd", ms * 0.8)):
+            for label, v in (("torch_eager", ms), ("kernelforge", ms * 0.8)):
                 db.record(run, p, Measurement(label=label, status="ok", verification=_ok(),
                                               timing=_timing(v), tflops=1.0))
         art = report.generate(db, tmp_path / "out")
@@ -118,7 +118,7 @@ def test_mixed_timing_methods_are_flagged(tmp_path):
         p = Problem.create("vector_add", "fp32", n=1 << 20)
         db.record(run, p, Measurement(label="torch_eager", status="ok", verification=_ok(),
                                       timing=_timing(0.01), gbps=1.0))
-        db.record(run, p, Measurement(label="kernelo_amd", status="ok", verification=_ok(),
+        db.record(run, p, Measurement(label="kernelforge", status="ok", verification=_ok(),
                                       timing=_timing(0.01, flushed=False), gbps=1.0))
         db.record(run, p, Measurement(label="torch_cpu", status="ok", verification=_ok(),
                                       timing=_timing(2.0, flushed=False, timer="perf_counter"),
@@ -149,7 +149,7 @@ def test_incorrect_rows_never_reach_a_table(tmp_path):
         run = db.start_run(capture_environment())
         p = Problem.create("matmul", "fp16", M=256, N=256, K=256)
         db.record(run, p, Measurement(
-            label="kernelo_amd", status="incorrect",
+            label="kernelforge", status="incorrect",
             verification=VerificationResult(False, 1.0, 1.0, 50, 100, 5e-3, "wrong"),
             timing=_timing(0.0123)))
         db.record(run, p, Measurement(label="torch_eager", status="ok", verification=_ok(),
@@ -175,7 +175,7 @@ def test_cli_report_renders_a_seeded_database(seeded, tmp_path):
 
     path = seeded.path
     out = subprocess.run(
-        [sys.executable, "-m", "kernelo_amd", "report", "--db", str(path), "--out",
+        [sys.executable, "-m", "kernelforge", "report", "--db", str(path), "--out",
          str(tmp_path / "cli")],
         capture_output=True, text=True, timeout=300,
     )

@@ -15,9 +15,9 @@ from __future__ import annotations
 import pytest
 import torch
 
-from kernelo_amd.runtime.env import MI355X_CAPS
-from kernelo_amd.tuning.config import KernelConfig, Problem
-from kernelo_amd.tuning.search import (
+from kernelforge.runtime.env import MI355X_CAPS
+from kernelforge.tuning.config import KernelConfig, Problem
+from kernelforge.tuning.search import (
     TWO_PASS_MAX_STAGED_BYTES,
     VectorAddSearchSpace,
     two_pass_block,
@@ -367,7 +367,7 @@ def test_two_pass_rules():
 @pytest.mark.parametrize("cols", [16385, 32768, 40704, 40705, 1 << 20])
 @pytest.mark.parametrize("dtype", ["fp32", "fp16", "bf16"])
 def test_default_config_past_the_limit_is_a_feasible_two_pass_config(cols, dtype):
-    from kernelo_amd.dtypes import itemsize, parse_dtype
+    from kernelforge.dtypes import itemsize, parse_dtype
 
     cfg = default_row_config("rmsnorm", cols, parse_dtype(dtype))
     assert cfg["TWO_PASS"] == 1
