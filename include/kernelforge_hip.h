@@ -88,6 +88,12 @@ const char* kf_build_target(void);
 /* Message describing the last failure on the calling thread ("" if none). */
 const char* kf_last_error(void);
 
+/* The id of the graph capture `stream` is in (0 when it is not capturing),
+ * from hipStreamGetCaptureInfo. Support for callers that keep split-K
+ * workspaces per capture; no counterpart in the reference (Triton launches are
+ * never captured there). */
+int kf_stream_capture_id(void* stream, unsigned long long* id);
+
 /*
  * Tiled MFMA GEMM, optionally with the fused bias + tanh-GELU epilogue.
  * Replaces matmul() (kernels/matmul.py:132-155) and fused_linear_gelu()

@@ -29,8 +29,24 @@ int launch_status(const char* what) {
 
 }  // namespace kf
 
-extern "C" int kf_abi_version(void) { return 4; }
+extern "C" int kf_abi_version(void) { return 5; }
 
 extern "C" const char* kf_build_target(void) { return "gfx950"; }
 
 extern "C" const char* kf_last_error(void) { return kf::g_last_error; }
+
+extern "C" int kf_stream_capture_id(void* stream, unsigned long long* id) {
+  if (id == nullptr) {
+    kf::set_error("stream_capture_id: null output");
+    return KF_ERR_INVALID_ARGUMENT;
+  }
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  unsigned long long seq = 0;
+  const hipError_t err = hipStreamGetCaptureInfo(static_cast<hipStream_t>(stream), &status, &seq);
+  if (err != hipSuccess) {
+    kf::set_error("stream_capture_id: %s", hipGetErrorName(err));
+    return KF_ERR_LAUNCH;
+  }
+  *id = status == hipStreamCaptureStatusActive ? seq : 0;
+  return KF_OK;
+}

@@ -1,11 +1,21 @@
-"""SQLite store for tuning and benchmark results.
+"""SQLite results store for tuning and benchmark runs.
 
-Same role and schema shape as the reference (kernelforge/db.py:35-320): runs
-carry provenance, problems and configs are deduplicated (configs by their
-JSON parameter set and digest), and results point at all three. Columns name
-what this build records: ``hip_version`` and ``cu_count`` where the reference
-stored CUDA/Triton versions and an SM count. The schema version lives in
-``PRAGMA user_version`` and a mismatch is refused rather than migrated.
+Every result row points at the run that produced it (host, GPU, HIP, torch and
+package versions), the problem, and the configuration, so a number from last
+week stays comparable -- or visibly not -- with one from today. The tables are
+the reference's (kernelforge/db.py:35-99) so existing report queries keep
+working; the vendor-specific provenance columns name what this build records
+(``hip_version`` and ``cu_count`` in place of CUDA/Triton versions and an SM
+count).
+
+Here the schema is data: each table is a tuple of column declarations from
+which the DDL and every INSERT are generated, so a column cannot be added to
+one and forgotten in the other. Problems and configurations are interned
+(insert-or-ignore on their natural key, then look the id up). A measurement is
+flattened into columns by small per-part functions (timing, verification), and
+a batch of measurements is one transaction. "Best per label" is one windowed
+query. The schema version lives in ``PRAGMA user_version``; a file written by
+another version is refused, not migrated.
 """
 
 from __future__ import annotations
@@ -13,8 +23,9 @@ from __future__ import annotations
 import json
 import os
 import sqlite3
-from collections.abc import Iterable
-from dataclasses import dataclass
+from collections.abc import Iterable, Iterator
+from contextlib import contextmanager
+from dataclasses import asdict, dataclass
 from pathlib import Path
 from typing import Any
 
@@ -25,85 +36,111 @@ from kernelforge.tuning.config import KernelConfig, Problem
 SCHEMA_VERSION = 1
 DEFAULT_DB_PATH = Path("results/kernelforge.db")
 
-_SCHEMA = """
-CREATE TABLE IF NOT EXISTS runs (
-    run_id              INTEGER PRIMARY KEY AUTOINCREMENT,
-    timestamp           TEXT    NOT NULL,
-    hostname            TEXT,
-    platform            TEXT,
-    python_version      TEXT,
-    torch_version       TEXT,
-    hip_version         TEXT,
-    driver_version      TEXT,
-    gpu_name            TEXT,
-    gpu_arch            TEXT,
-    gpu_memory_bytes    INTEGER,
-    cu_count            INTEGER,
-    device_key          TEXT    NOT NULL,
-    package_version     TEXT,
-    notes               TEXT    NOT NULL DEFAULT ''
-);
+_Columns = tuple[tuple[str, str], ...]
 
-CREATE TABLE IF NOT EXISTS problems (
-    problem_id INTEGER PRIMARY KEY AUTOINCREMENT,
-    operation  TEXT NOT NULL,
-    shape_key  TEXT NOT NULL,
-    dtype      TEXT NOT NULL,
-    dims_json  TEXT NOT NULL,
-    UNIQUE (operation, shape_key, dtype)
-);
+#: table -> (columns, table constraints); the first column is the row id.
+_TABLES: dict[str, tuple[_Columns, tuple[str, ...]]] = {
+    "runs": (
+        (
+            ("run_id", "INTEGER PRIMARY KEY AUTOINCREMENT"),
+            ("timestamp", "TEXT NOT NULL"),
+            ("hostname", "TEXT"),
+            ("platform", "TEXT"),
+            ("python_version", "TEXT"),
+            ("torch_version", "TEXT"),
+            ("hip_version", "TEXT"),
+            ("driver_version", "TEXT"),
+            ("gpu_name", "TEXT"),
+            ("gpu_arch", "TEXT"),
+            ("gpu_memory_bytes", "INTEGER"),
+            ("cu_count", "INTEGER"),
+            ("device_key", "TEXT NOT NULL"),
+            ("package_version", "TEXT"),
+            ("notes", "TEXT NOT NULL DEFAULT ''"),
+        ),
+        (),
+    ),
+    "problems": (
+        (
+            ("problem_id", "INTEGER PRIMARY KEY AUTOINCREMENT"),
+            ("operation", "TEXT NOT NULL"),
+            ("shape_key", "TEXT NOT NULL"),
+            ("dtype", "TEXT NOT NULL"),
+            ("dims_json", "TEXT NOT NULL"),
+        ),
+        ("UNIQUE (operation, shape_key, dtype)",),
+    ),
+    "configs": (
+        (
+            ("config_id", "INTEGER PRIMARY KEY AUTOINCREMENT"),
+            ("operation", "TEXT NOT NULL"),
+            ("digest", "TEXT NOT NULL"),
+            ("params_json", "TEXT NOT NULL"),
+        ),
+        ("UNIQUE (operation, digest)",),
+    ),
+    "results": (
+        (
+            ("result_id", "INTEGER PRIMARY KEY AUTOINCREMENT"),
+            ("run_id", "INTEGER NOT NULL REFERENCES runs (run_id)"),
+            ("problem_id", "INTEGER NOT NULL REFERENCES problems (problem_id)"),
+            ("config_id", "INTEGER REFERENCES configs (config_id)"),
+            ("label", "TEXT NOT NULL"),
+            ("status", "TEXT NOT NULL"),
+            ("correct", "INTEGER"),
+            ("rel_error", "REAL"),
+            ("median_us", "REAL"),
+            ("mean_us", "REAL"),
+            ("std_us", "REAL"),
+            ("min_us", "REAL"),
+            ("max_us", "REAL"),
+            ("p95_us", "REAL"),
+            ("p99_us", "REAL"),
+            ("warmup", "INTEGER"),
+            ("iterations", "INTEGER"),
+            ("timer", "TEXT"),
+            ("flushed_l2", "INTEGER"),
+            ("tflops", "REAL"),
+            ("gbps", "REAL"),
+            ("error", "TEXT NOT NULL DEFAULT ''"),
+        ),
+        (),
+    ),
+}
 
-CREATE TABLE IF NOT EXISTS configs (
-    config_id   INTEGER PRIMARY KEY AUTOINCREMENT,
-    operation   TEXT NOT NULL,
-    digest      TEXT NOT NULL,
-    params_json TEXT NOT NULL,
-    UNIQUE (operation, digest)
-);
+_INDEXES = (
+    "CREATE INDEX IF NOT EXISTS idx_results_problem ON results (problem_id, label)",
+    "CREATE INDEX IF NOT EXISTS idx_results_run ON results (run_id)",
+)
 
-CREATE TABLE IF NOT EXISTS results (
-    result_id  INTEGER PRIMARY KEY AUTOINCREMENT,
-    run_id     INTEGER NOT NULL REFERENCES runs (run_id),
-    problem_id INTEGER NOT NULL REFERENCES problems (problem_id),
-    config_id  INTEGER          REFERENCES configs (config_id),
-    label      TEXT    NOT NULL,
-    status     TEXT    NOT NULL,
-    correct    INTEGER,
-    rel_error  REAL,
-    median_us  REAL,
-    mean_us    REAL,
-    std_us     REAL,
-    min_us     REAL,
-    max_us     REAL,
-    p95_us     REAL,
-    p99_us     REAL,
-    warmup     INTEGER,
-    iterations INTEGER,
-    timer      TEXT,
-    flushed_l2 INTEGER,
-    tflops     REAL,
-    gbps       REAL,
-    error      TEXT NOT NULL DEFAULT ''
-);
 
-CREATE INDEX IF NOT EXISTS idx_results_problem ON results (problem_id, label);
-CREATE INDEX IF NOT EXISTS idx_results_run     ON results (run_id);
-"""
+def _ddl() -> str:
+    statements = []
+    for table, (columns, constraints) in _TABLES.items():
+        body = [f"{name} {decl}" for name, decl in columns] + list(constraints)
+        statements.append(f"CREATE TABLE IF NOT EXISTS {table} ({', '.join(body)})")
+    return ";\n".join(statements + list(_INDEXES)) + ";"
 
-_ROWS_QUERY = """
-SELECT
-    r.result_id, r.label, r.status, r.correct, r.rel_error,
-    r.median_us, r.mean_us, r.std_us, r.min_us, r.max_us, r.p95_us, r.p99_us,
-    r.warmup, r.iterations, r.timer, r.flushed_l2, r.tflops, r.gbps, r.error,
-    p.operation, p.shape_key, p.dtype, p.dims_json,
-    c.params_json, c.digest,
-    run.run_id, run.timestamp, run.gpu_name, run.gpu_arch, run.device_key,
-    run.torch_version, run.hip_version, run.driver_version
-FROM results AS r
-JOIN problems AS p   ON p.problem_id = r.problem_id
-JOIN runs     AS run ON run.run_id   = r.run_id
-LEFT JOIN configs AS c ON c.config_id = r.config_id
-"""
+
+def _insertable(table: str) -> tuple[str, ...]:
+    """Columns an INSERT names: all but the auto-assigned id."""
+    return tuple(name for name, _ in _TABLES[table][0][1:])
+
+
+#: The joined view every read returns: result, problem, config and run provenance.
+_JOINED = {
+    "r": ("result_id", "label", "status", "correct", "rel_error", "median_us", "mean_us", "std_us",
+          "min_us", "max_us", "p95_us", "p99_us", "warmup", "iterations", "timer", "flushed_l2",
+          "tflops", "gbps", "error"),
+    "p": ("operation", "shape_key", "dtype", "dims_json"),
+    "c": ("params_json", "digest"),
+    "run": ("run_id", "timestamp", "gpu_name", "gpu_arch", "device_key", "torch_version",
+            "hip_version", "driver_version"),
+}
+_FROM = ("FROM results AS r JOIN problems AS p ON p.problem_id = r.problem_id "
+         "JOIN runs AS run ON run.run_id = r.run_id "
+         "LEFT JOIN configs AS c ON c.config_id = r.config_id")
+_SELECT = "SELECT " + ", ".join(f"{alias}.{col}" for alias, cols in _JOINED.items() for col in cols)
 
 
 @dataclass(frozen=True)
@@ -114,39 +151,55 @@ class Measurement:
     status: str
     config: KernelConfig | None = None
     verification: VerificationResult | None = None
-    timing: Any = None  # TimingResult (kept loose so this module stays import-light)
+    timing: Any = None  # a TimingResult; typed loosely so this module needs no GPU imports
     tflops: float | None = None
     gbps: float | None = None
     error: str = ""
 
 
+def _timing_columns(timing: Any) -> dict[str, Any]:
+    stats_us = ("median", "mean", "std", "min", "max", "p95", "p99")
+    if timing is None:
+        return {**{f"{s}_us": None for s in stats_us},
+                "warmup": None, "iterations": None, "timer": None, "flushed_l2": None}
+    out: dict[str, Any] = {f"{s}_us": getattr(timing, f"{s}_ms") * 1e3 for s in stats_us}
+    out.update(warmup=timing.warmup, iterations=timing.iterations, timer=timing.timer,
+               flushed_l2=int(bool(timing.flushed_l2)))
+    return out
+
+
+def _verification_columns(result: VerificationResult | None) -> dict[str, Any]:
+    if result is None:
+        return {"correct": None, "rel_error": None}
+    return {"correct": int(result.passed), "rel_error": result.error}
+
+
 def default_db_path() -> Path:
-    return Path(os.environ.get("KERNELO_AMD_DB", os.environ.get("KERNELFORGE_DB", DEFAULT_DB_PATH)))
+    """``$KERNELFORGE_DB``, else ``results/kernelforge.db`` under the working directory."""
+    return Path(os.environ.get("KERNELFORGE_DB") or DEFAULT_DB_PATH)
 
 
 class ResultsDB:
-    """Explicit wrapper over the results database."""
+    """The results database behind ``tune``, ``benchmark``, ``compare`` and ``report``."""
 
     def __init__(self, path: str | Path | None = None) -> None:
         self.path = Path(path) if path is not None else default_db_path()
-        if str(self.path) != ":memory:":
+        in_memory = str(self.path) == ":memory:"
+        if not in_memory:
             self.path.parent.mkdir(parents=True, exist_ok=True)
         self._conn = sqlite3.connect(str(self.path))
         self._conn.row_factory = sqlite3.Row
         self._conn.execute("PRAGMA foreign_keys = ON")
-        self._conn.executescript(_SCHEMA)
-        self._check_schema_version()
-        self._conn.commit()
-
-    def _check_schema_version(self) -> None:
-        current = int(self._conn.execute("PRAGMA user_version").fetchone()[0])
-        if current == 0:
-            self._conn.execute(f"PRAGMA user_version = {SCHEMA_VERSION}")
-        elif current != SCHEMA_VERSION:
+        version = int(self._conn.execute("PRAGMA user_version").fetchone()[0])
+        if version not in (0, SCHEMA_VERSION):
+            self._conn.close()
             raise RuntimeError(
-                f"{self.path} was written by schema version {current}, "
+                f"{self.path} was written by schema version {version}, "
                 f"this build expects {SCHEMA_VERSION}"
             )
+        with self._conn:
+            self._conn.executescript(_ddl())
+            self._conn.execute(f"PRAGMA user_version = {SCHEMA_VERSION}")
 
     def __enter__(self) -> ResultsDB:
         return self
@@ -157,142 +210,116 @@ class ResultsDB:
     def close(self) -> None:
         self._conn.close()
 
-    # --- writes ---------------------------------------------------------------
-    def start_run(self, env: Environment, *, notes: str = "", version: str = "") -> int:
-        cur = self._conn.execute(
-            """
-            INSERT INTO runs (
-                timestamp, hostname, platform, python_version, torch_version, hip_version,
-                driver_version, gpu_name, gpu_arch, gpu_memory_bytes, cu_count, device_key,
-                package_version, notes
-            ) VALUES (?,?,?,?,?,?,?,?,?,?,?,?,?,?)
-            """,
-            (
-                env.timestamp,
-                env.hostname,
-                env.platform,
-                env.python_version,
-                env.torch_version,
-                env.hip_version,
-                env.driver_version,
-                env.gpu_name,
-                env.gpu_arch,
-                env.gpu_memory_bytes,
-                env.cu_count,
-                env.device_key,
-                version,
-                notes,
-            ),
+    # --- writes -------------------------------------------------------------------
+    @contextmanager
+    def _transaction(self) -> Iterator[sqlite3.Connection]:
+        with self._conn:  # commits on success, rolls back on error
+            yield self._conn
+
+    def _insert(self, table: str, values: dict[str, Any]) -> int:
+        names = [c for c in _insertable(table) if c in values]
+        sql = f"INSERT INTO {table} ({', '.join(names)}) VALUES ({', '.join('?' * len(names))})"
+        return int(self._conn.execute(sql, [values[c] for c in names]).lastrowid)
+
+    def _intern(self, table: str, natural_key: dict[str, Any], extra: dict[str, Any]) -> int:
+        """Id of the row with ``natural_key``, inserting it (with ``extra``) if new."""
+        id_col = _TABLES[table][0][0][0]
+        names = list(natural_key) + list(extra)
+        self._conn.execute(
+            f"INSERT OR IGNORE INTO {table} ({', '.join(names)}) "
+            f"VALUES ({', '.join('?' * len(names))})",
+            [*natural_key.values(), *extra.values()],
         )
-        self._conn.commit()
-        return int(cur.lastrowid)
+        where = " AND ".join(f"{k} = ?" for k in natural_key)
+        row = self._conn.execute(f"SELECT {id_col} FROM {table} WHERE {where}",
+                                 list(natural_key.values())).fetchone()
+        return int(row[0])
+
+    def start_run(self, env: Environment, *, notes: str = "", version: str = "") -> int:
+        """Record the environment of a run; its id tags every result of that run."""
+        values = {k: v for k, v in asdict(env).items() if k in _insertable("runs")}
+        values.update(package_version=version, notes=notes)
+        with self._transaction():
+            return self._insert("runs", values)
 
     def problem_id(self, problem: Problem) -> int:
-        self._conn.execute(
-            "INSERT OR IGNORE INTO problems (operation, shape_key, dtype, dims_json) "
-            "VALUES (?,?,?,?)",
-            (
-                problem.operation,
-                problem.shape_key,
-                problem.dtype_name,
-                json.dumps(problem.dims_dict, sort_keys=True),
-            ),
-        )
-        row = self._conn.execute(
-            "SELECT problem_id FROM problems WHERE operation=? AND shape_key=? AND dtype=?",
-            (problem.operation, problem.shape_key, problem.dtype_name),
-        ).fetchone()
-        return int(row["problem_id"])
+        with self._transaction():
+            return self._intern(
+                "problems",
+                {"operation": problem.operation, "shape_key": problem.shape_key,
+                 "dtype": problem.dtype_name},
+                {"dims_json": json.dumps(problem.dims_dict, sort_keys=True)},
+            )
 
     def config_id(self, config: KernelConfig) -> int:
-        self._conn.execute(
-            "INSERT OR IGNORE INTO configs (operation, digest, params_json) VALUES (?,?,?)",
-            (config.operation, config.digest, config.to_json()),
-        )
-        row = self._conn.execute(
-            "SELECT config_id FROM configs WHERE operation=? AND digest=?",
-            (config.operation, config.digest),
-        ).fetchone()
-        return int(row["config_id"])
+        with self._transaction():
+            return self._intern("configs", {"operation": config.operation, "digest": config.digest},
+                                {"params_json": config.to_json()})
+
+    def _result(self, run_id: int, problem_id: int, m: Measurement) -> int:
+        config_id = None
+        if m.config is not None:
+            config_id = self._intern("configs", {"operation": m.config.operation,
+                                                 "digest": m.config.digest},
+                                     {"params_json": m.config.to_json()})
+        values = {"run_id": run_id, "problem_id": problem_id, "config_id": config_id,
+                  "label": m.label, "status": m.status, "tflops": m.tflops, "gbps": m.gbps,
+                  "error": m.error}
+        values.update(_verification_columns(m.verification))
+        values.update(_timing_columns(m.timing))
+        return self._insert("results", values)
+
+    def record_many(self, run_id: int, problem: Problem, measurements: Iterable[Measurement]) -> list[int]:
+        """Record several measurements of one problem in one transaction."""
+        pid = self.problem_id(problem)
+        with self._transaction():
+            return [self._result(run_id, pid, m) for m in measurements]
 
     def record(self, run_id: int, problem: Problem, measurement: Measurement) -> int:
-        t = measurement.timing
-        v = measurement.verification
-        us = (lambda ms: None if t is None else ms * 1e3)
-        cur = self._conn.execute(
-            """
-            INSERT INTO results (
-                run_id, problem_id, config_id, label, status, correct, rel_error,
-                median_us, mean_us, std_us, min_us, max_us, p95_us, p99_us,
-                warmup, iterations, timer, flushed_l2, tflops, gbps, error
-            ) VALUES (?,?,?,?,?,?,?,?,?,?,?,?,?,?,?,?,?,?,?,?,?)
-            """,
-            (
-                run_id,
-                self.problem_id(problem),
-                self.config_id(measurement.config) if measurement.config is not None else None,
-                measurement.label,
-                measurement.status,
-                None if v is None else int(v.passed),
-                None if v is None else v.error,
-                us(t.median_ms) if t else None,
-                us(t.mean_ms) if t else None,
-                us(t.std_ms) if t else None,
-                us(t.min_ms) if t else None,
-                us(t.max_ms) if t else None,
-                us(t.p95_ms) if t else None,
-                us(t.p99_ms) if t else None,
-                None if t is None else t.warmup,
-                None if t is None else t.iterations,
-                None if t is None else t.timer,
-                None if t is None else int(t.flushed_l2),
-                measurement.tflops,
-                measurement.gbps,
-                measurement.error,
-            ),
-        )
-        self._conn.commit()
-        return int(cur.lastrowid)
+        return self.record_many(run_id, problem, [measurement])[0]
 
-    def record_many(self, run_id: int, problem: Problem, measurements: Iterable[Measurement]) -> None:
-        for m in measurements:
-            self.record(run_id, problem, m)
+    # --- reads --------------------------------------------------------------------
+    def _select(self, where: dict[str, str | None], tail: str) -> list[dict]:
+        active = {col: val for col, val in where.items() if val}
+        sql = f"{_SELECT} {_FROM}"
+        if active:
+            sql += " WHERE " + " AND ".join(f"{col} = ?" for col in active)
+        return [dict(r) for r in self._conn.execute(f"{sql} {tail}", list(active.values()))]
 
-    # --- reads ----------------------------------------------------------------
     def rows(self, *, operation: str | None = None, dtype: str | None = None) -> list[dict]:
-        clauses, params = [], []
-        if operation:
-            clauses.append("p.operation = ?")
-            params.append(operation)
-        if dtype:
-            clauses.append("p.dtype = ?")
-            params.append(dtype)
-        query = _ROWS_QUERY
-        if clauses:
-            query += " WHERE " + " AND ".join(clauses)
-        query += " ORDER BY r.result_id"
-        return [dict(row) for row in self._conn.execute(query, params)]
+        """Every result joined with its problem, config and run, in insertion order."""
+        return self._select({"p.operation": operation, "p.dtype": dtype}, "ORDER BY r.result_id")
 
     def best_per_label(self, *, operation: str | None = None) -> list[dict]:
-        """Fastest correct measurement for each (problem, label) pair."""
-        best: dict[tuple[str, str, str, str], dict] = {}
-        for row in self.rows(operation=operation):
-            if row["median_us"] is None or row["correct"] == 0:
-                continue
-            key = (row["operation"], row["shape_key"], row["dtype"], row["label"])
-            if key not in best or row["median_us"] < best[key]["median_us"]:
-                best[key] = row
-        return sorted(
-            best.values(), key=lambda r: (r["operation"], r["dtype"], r["shape_key"], r["label"])
+        """The fastest timed, not-incorrect result of each (problem, label).
+
+        Rows without a timing or whose verification failed never win; ties go
+        to the earlier row.
+        """
+        ranked = (
+            f"{_SELECT}, ROW_NUMBER() OVER (PARTITION BY r.problem_id, r.label "
+            f"ORDER BY r.median_us, r.result_id) AS rank_in_label {_FROM} "
+            "WHERE r.median_us IS NOT NULL AND (r.correct IS NULL OR r.correct != 0)"
         )
+        args: list[str] = []
+        if operation:
+            ranked += " AND p.operation = ?"
+            args.append(operation)
+        sql = (f"SELECT * FROM ({ranked}) WHERE rank_in_label = 1 "
+               "ORDER BY operation, dtype, shape_key, label")
+        out = [dict(r) for r in self._conn.execute(sql, args)]
+        for row in out:
+            row.pop("rank_in_label")
+        return out
 
     def runs(self) -> list[dict]:
-        """Every recorded run, oldest first (including runs that recorded nothing)."""
-        return [dict(row) for row in self._conn.execute("SELECT * FROM runs ORDER BY run_id")]
+        """Every recorded run, oldest first, including runs that recorded nothing."""
+        return [dict(r) for r in self._conn.execute("SELECT * FROM runs ORDER BY run_id")]
 
     def counts(self) -> dict[str, int]:
-        tables = ("runs", "problems", "configs", "results")
-        return {t: int(self._conn.execute(f"SELECT COUNT(*) FROM {t}").fetchone()[0]) for t in tables}
+        return {t: int(self._conn.execute(f"SELECT COUNT(*) FROM {t}").fetchone()[0])
+                for t in _TABLES}
 
     def operations(self) -> list[str]:
-        return [r[0] for r in self._conn.execute("SELECT DISTINCT operation FROM problems ORDER BY 1")]
+        return [r[0] for r in self._conn.execute(
+            "SELECT DISTINCT operation FROM problems ORDER BY operation")]

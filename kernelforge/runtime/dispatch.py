@@ -48,7 +48,7 @@ def packaged_cache() -> ConfigCache | None:
     """The winners shipped with the package (read-only), if present."""
     global _PACKAGED
     if _PACKAGED is None and PACKAGED_CACHE.exists():
-        _PACKAGED = ConfigCache(PACKAGED_CACHE)
+        _PACKAGED = ConfigCache(PACKAGED_CACHE, read_only=True)
     return _PACKAGED
 
 

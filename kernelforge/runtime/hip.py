@@ -36,6 +36,8 @@ KF_EPILOGUE_BIAS_GELU = 1
 KF_PIPELINE_STAGED = 0
 KF_PIPELINE_DIRECT = 1
 
+KF_WORKSPACE_COUNTER_BYTES = 4 << 18
+
 
 class KernelError(RuntimeError):
     """A status code other than KF_OK from the C-ABI."""
@@ -95,6 +97,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "kf_abi_version": (_int, []),
     "kf_build_target": (ctypes.c_char_p, []),
     "kf_last_error": (ctypes.c_char_p, []),
+    "kf_stream_capture_id": (_int, [_vp, ctypes.POINTER(ctypes.c_ulonglong)]),
     "kf_gemm": (
         _int,
         [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int,
@@ -134,7 +137,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
 }
 
 #: kf_abi_version() of the library these signatures describe.
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -218,27 +221,62 @@ def gemm_variants() -> list[tuple[int, int, int, int, int, int, int]]:
     return out
 
 
+def capture_id(stream: int) -> int:
+    """Id of the graph capture ``stream`` is recording into, 0 when it is not capturing."""
+    out = ctypes.c_ulonglong(0)
+    check(load().kf_stream_capture_id(stream, ctypes.byref(out)), "stream capture query")
+    return out.value
+
+
 class _Workspaces:
-    """Per (device, stream) split-K workspace, zeroed when (re)allocated.
+    """Split-K workspaces: one per (device, stream) for eager calls, one per
+    (device, stream, capture) for calls recorded into a HIP graph.
 
     Every split-K entry point (GEMV and GEMM) lays a workspace out the same
     way: a fixed region of arrival counters, then fp32 partial sums. The
-    counters must start at zero and each completed call returns them to zero;
-    since their region is the same for every shape, one buffer serves any
-    sequence of calls on its stream and only needs clearing when it is made.
+    counters must be zero when a call starts and every completed call returns
+    them to zero, so one buffer serves any sequence of calls in stream order.
+
+    Eager buffers are cleared when made and replaced (the old one freed) when a
+    call needs more; stream order makes both safe.
+
+    A graph replays its kernels on the addresses it captured, long after the
+    capture, and may be replayed on other streams. So a capture gets buffers of
+    its own: created inside the capture (from the graph's memory pool), cleared
+    by a fill node recorded at that point (so every replay starts from zero
+    counters), shared only by later calls of the same capture, and never
+    released: this object keeps a reference for the life of the process, so no
+    later allocation can take memory a graph still writes. Two replays of one
+    graph running at the same time share its buffers and race, like any
+    concurrent use of one workspace.
     """
 
     def __init__(self) -> None:
-        self._bufs: dict[tuple[int, int], torch.Tensor] = {}
+        self._eager: dict[tuple[int, int], torch.Tensor] = {}
+        self._captured: dict[tuple[int, int, int], torch.Tensor] = {}
+        self._held: list[torch.Tensor] = []
 
     def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-        key = (device.index or 0, stream)
-        buf = self._bufs.get(key)
+        dev = device.index if device.index is not None else torch.cuda.current_device()
+        cap = capture_id(stream)
+        if cap:
+            key = (dev, stream, cap)
+            buf = self._captured.get(key)
+            if buf is None or buf.numel() < nbytes:
+                buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+                self._captured[key] = buf
+                self._held.append(buf)
+            return buf
+        key = (dev, stream)
+        buf = self._eager.get(key)
         if buf is None or buf.numel() < nbytes:
-            size = max(nbytes, 1 << 20)
-            buf = torch.zeros(size, dtype=torch.uint8, device=device)
-            self._bufs[key] = buf
+            buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            self._eager[key] = buf
         return buf
+
+    def held_for_graphs(self) -> int:
+        """Bytes kept alive for captured graphs."""
+        return sum(b.numel() for b in self._held)
 
 
 workspaces = _Workspaces()

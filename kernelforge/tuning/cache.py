@@ -1,12 +1,23 @@
-"""Persistent winner cache: ``device_key -> operation -> dtype -> shape_key``.
+"""The JSON winner cache: best-known configuration per device, op, dtype and shape.
 
-A serving process must not re-tune on start-up, so the winning configuration
-is written to a JSON file and reused for an identical problem on an
-identical device (kernelforge/tuning/cache.py:1-159). The device key is the
-board name plus the architecture (``AMD_Instinct_MI355X_gfx950``), so a file
-copied to other hardware misses instead of serving a foreign winner. Writes
-go through a temporary file and ``os.replace``; an unknown version is
-refused.
+Tuning costs minutes; a serving process reads its winners from this file in
+microseconds and never tunes (kernelforge/tuning/cache.py:1-159). The file
+format is the reference's, so cache files move between the two tools::
+
+    {"version": 1,
+     "entries": {<device key>: {<operation>: {<dtype>: {<shape key>:
+         {"config": {...}, "median_us": ..., "timestamp": ..., "candidates_tested": ...}}}}}}
+
+The device key is the board plus the architecture
+(``AMD_Instinct_MI355X_gfx950``): a file copied to other hardware misses rather
+than serving a winner tuned elsewhere.
+
+In memory the nesting is flattened to one index keyed by
+``(device, operation, dtype, shape)``; the nested form exists only on disk.
+Every change is written through a temporary file in the same directory and
+``os.replace``, so a reader never sees a half-written file. Two files are
+consulted by dispatch: the user's (read-write) and the winners packaged with
+this build (read-only).
 """
 
 from __future__ import annotations
@@ -16,24 +27,31 @@ import os
 import tempfile
 from dataclasses import dataclass
 from pathlib import Path
-from typing import Any
+from typing import Any, NamedTuple
 
 from kernelforge.tuning.config import KernelConfig, Problem
 
 CACHE_VERSION = 1
 
-
-#: Winners tuned on MI355X and shipped with the package; consulted by
-#: dispatch after the user's cache, never written at run time.
+#: Winners tuned on MI355X and shipped with the package; dispatch consults them
+#: after the user's cache and nothing writes them at run time.
 PACKAGED_CACHE = Path(__file__).resolve().parent.parent / "tuned" / "mi355x_gfx950.json"
 
 
 def default_cache_path() -> Path:
-    for var in ("KERNELO_AMD_CACHE", "KERNELFORGE_CACHE"):
-        if env := os.environ.get(var):
-            return Path(env)
-    root = Path(os.environ.get("XDG_CACHE_HOME", Path.home() / ".cache"))
-    return root / "kernelforge" / "configs.json"
+    """``$KERNELFORGE_CACHE``, else ``$XDG_CACHE_HOME/kernelforge/configs.json``."""
+    explicit = os.environ.get("KERNELFORGE_CACHE")
+    if explicit:
+        return Path(explicit)
+    base = os.environ.get("XDG_CACHE_HOME") or str(Path.home() / ".cache")
+    return Path(base) / "kernelforge" / "configs.json"
+
+
+class _Key(NamedTuple):
+    device_key: str
+    operation: str
+    dtype: str
+    shape_key: str
 
 
 @dataclass(frozen=True)
@@ -48,58 +66,85 @@ class CacheEntry:
     candidates_tested: int | None = None
 
     def describe(self) -> str:
-        params = ", ".join(f"{k}={v}" for k, v in self.config.as_dict().items())
-        latency = f"{self.median_us:.1f} us" if self.median_us is not None else "unmeasured"
-        return (
-            f"{self.device_key}  {self.operation:<13} {self.dtype:<5} "
-            f"{self.shape_key:<22} {latency:>12}  {params}"
-        )
+        """One aligned line for ``kernelforge cache list``."""
+        took = "unmeasured" if self.median_us is None else f"{self.median_us:.1f} us"
+        params = ", ".join(f"{k}={v}" for k, v in self.config.items())
+        return (f"{self.device_key}  {self.operation:<13} {self.dtype:<5} {self.shape_key:<22} "
+                f"{took:>12}  {params}")
+
+
+def _flatten(document: dict[str, Any]) -> dict[_Key, dict[str, Any]]:
+    flat: dict[_Key, dict[str, Any]] = {}
+    for device, per_op in document.get("entries", {}).items():
+        for operation, per_dtype in per_op.items():
+            for dtype, per_shape in per_dtype.items():
+                for shape, record in per_shape.items():
+                    flat[_Key(device, operation, dtype, shape)] = record
+    return flat
+
+
+def _nest(flat: dict[_Key, dict[str, Any]]) -> dict[str, Any]:
+    entries: dict[str, Any] = {}
+    for key in sorted(flat):
+        level = entries
+        for part in key[:-1]:
+            level = level.setdefault(part, {})
+        level[key.shape_key] = flat[key]
+    return {"version": CACHE_VERSION, "entries": entries}
 
 
 class ConfigCache:
-    """A JSON file of best-known configurations."""
+    """One winner file. ``read_only`` caches refuse ``put`` and ``clear``."""
 
-    def __init__(self, path: str | Path | None = None) -> None:
+    def __init__(self, path: str | Path | None = None, *, read_only: bool = False) -> None:
         self.path = Path(path) if path is not None else default_cache_path()
-        self._data = self._load()
+        self.read_only = read_only
+        self._records = self._read()
 
-    def _load(self) -> dict[str, Any]:
-        if not self.path.exists():
-            return {"version": CACHE_VERSION, "entries": {}}
+    def _read(self) -> dict[_Key, dict[str, Any]]:
         try:
-            data = json.loads(self.path.read_text())
+            text = self.path.read_text()
+        except FileNotFoundError:
+            return {}
+        try:
+            document = json.loads(text)
         except json.JSONDecodeError as exc:
             raise RuntimeError(f"cache file {self.path} is not valid JSON: {exc}") from exc
-        version = data.get("version") if isinstance(data, dict) else None
-        if version != CACHE_VERSION:
+        found = document.get("version") if isinstance(document, dict) else None
+        if found != CACHE_VERSION:
             raise RuntimeError(
-                f"cache file {self.path} has version {version}, expected {CACHE_VERSION}; "
+                f"cache file {self.path} has version {found}, expected {CACHE_VERSION}; "
                 "run `kernelforge cache clear` to discard it"
             )
-        return data
+        return _flatten(document)
 
-    def _flush(self) -> None:
+    def _write(self) -> None:
         self.path.parent.mkdir(parents=True, exist_ok=True)
-        fd, tmp = tempfile.mkstemp(dir=self.path.parent, suffix=".tmp")
+        payload = json.dumps(_nest(self._records), indent=2, sort_keys=True)
+        handle = tempfile.NamedTemporaryFile(
+            "w", dir=self.path.parent, prefix=f".{self.path.name}.", suffix=".tmp", delete=False
+        )
         try:
-            with os.fdopen(fd, "w") as handle:
-                json.dump(self._data, handle, indent=2, sort_keys=True)
-            os.replace(tmp, self.path)
+            with handle:
+                handle.write(payload)
+                handle.flush()
+                os.fsync(handle.fileno())
+            os.replace(handle.name, self.path)
         except BaseException:
-            Path(tmp).unlink(missing_ok=True)
+            Path(handle.name).unlink(missing_ok=True)
             raise
 
+    def _guard(self, what: str) -> None:
+        if self.read_only:
+            raise PermissionError(f"{self.path} is a read-only winner file; cannot {what}")
+
+    @staticmethod
+    def _key(problem: Problem, device_key: str) -> _Key:
+        return _Key(device_key, problem.operation, problem.dtype_name, problem.shape_key)
+
     def get(self, problem: Problem, device_key: str) -> KernelConfig | None:
-        node = (
-            self._data["entries"]
-            .get(device_key, {})
-            .get(problem.operation, {})
-            .get(problem.dtype_name, {})
-            .get(problem.shape_key)
-        )
-        if node is None:
-            return None
-        return KernelConfig(problem.operation, **node["config"])
+        record = self._records.get(self._key(problem, device_key))
+        return None if record is None else KernelConfig(problem.operation, **record["config"])
 
     def put(
         self,
@@ -111,43 +156,37 @@ class ConfigCache:
         timestamp: str = "",
         candidates_tested: int | None = None,
     ) -> None:
-        node = self._data["entries"].setdefault(device_key, {})
-        node = node.setdefault(problem.operation, {})
-        node = node.setdefault(problem.dtype_name, {})
-        node[problem.shape_key] = {
+        self._guard("store a winner")
+        self._records[self._key(problem, device_key)] = {
             "config": config.as_dict(),
             "median_us": median_us,
             "timestamp": timestamp,
             "candidates_tested": candidates_tested,
         }
-        self._flush()
+        self._write()
 
     def entries(self) -> list[CacheEntry]:
-        out: list[CacheEntry] = []
-        for device_key, operations in self._data["entries"].items():
-            for operation, dtypes in operations.items():
-                for dtype, shapes in dtypes.items():
-                    for shape_key, payload in shapes.items():
-                        out.append(
-                            CacheEntry(
-                                device_key=device_key,
-                                operation=operation,
-                                dtype=dtype,
-                                shape_key=shape_key,
-                                config=KernelConfig(operation, **payload["config"]),
-                                median_us=payload.get("median_us"),
-                                timestamp=payload.get("timestamp", ""),
-                                candidates_tested=payload.get("candidates_tested"),
-                            )
-                        )
-        return sorted(out, key=lambda e: (e.device_key, e.operation, e.dtype, e.shape_key))
+        return [
+            CacheEntry(
+                device_key=key.device_key,
+                operation=key.operation,
+                dtype=key.dtype,
+                shape_key=key.shape_key,
+                config=KernelConfig(key.operation, **record["config"]),
+                median_us=record.get("median_us"),
+                timestamp=record.get("timestamp", ""),
+                candidates_tested=record.get("candidates_tested"),
+            )
+            for key, record in sorted(self._records.items())
+        ]
 
     def clear(self) -> int:
-        removed = len(self.entries())
-        self._data = {"version": CACHE_VERSION, "entries": {}}
-        if self.path.exists():
-            self.path.unlink()
-        return removed
+        """Forget every entry and delete the file; returns how many there were."""
+        self._guard("clear it")
+        count = len(self._records)
+        self._records = {}
+        self.path.unlink(missing_ok=True)
+        return count
 
     def __len__(self) -> int:
-        return len(self.entries())
+        return len(self._records)

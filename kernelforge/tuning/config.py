@@ -1,13 +1,22 @@
-"""Problem and configuration descriptors.
+"""Descriptors: what is being run (``Problem``) and how (``KernelConfig``).
 
-Same identity semantics as the reference (kernelforge/tuning/config.py:33-150):
-a configuration is an immutable open mapping of int parameters whose JSON
-form and sha1 digest identify it in the results database, and a problem
-carries named dimensions that become cache keys.
+On this build a configuration does not parameterise a JIT compile; it names
+one ahead-of-time instantiation in ``libkernelforge_hip.so`` (tile shape,
+pipeline, stage count) plus the launch arguments the C-ABI takes for it
+(waves per workgroup, split-K, group size). Configurations stay open integer
+mappings, because the row kernels, the GEMV and the GEMM tiles have disjoint
+parameter sets.
 
-On gfx950 the "launch" keys are ``num_warps`` (wavefronts of 64 lanes per
-workgroup) and ``num_stages`` (LDS buffers); every other key selects a
-compile-time instantiation or a kernel argument.
+The interchange formats are the reference's, so results databases and cache
+files stay readable by either tool (kernelforge/tuning/config.py:33-150):
+
+* canonical JSON: keys sorted, no whitespace (``{"BLOCK_M":64,"num_warps":8}``);
+* digest: the first 16 hex digits of sha1 over ``"<operation>|<json>"``;
+* shape key: dimension values joined by ``x`` in declaration order, and the
+  cache key ``<operation>/<dtype>/<shape key>``.
+
+``num_warps`` counts 64-lane wavefronts and ``num_stages`` LDS buffers; they
+are the launch keys, everything else picks the instantiation.
 """
 
 from __future__ import annotations
@@ -15,101 +24,181 @@ from __future__ import annotations
 import hashlib
 import json
 from collections.abc import Iterator, Mapping
-from dataclasses import dataclass
 from typing import Any
 
 import torch
 
 from kernelforge.dtypes import dtype_name, itemsize, parse_dtype
 
-#: Parameters that shape the launch rather than the tile (config.py:30).
+#: Keys that describe the launch rather than the instantiation (config.py:30).
 LAUNCH_KEYS = frozenset({"num_warps", "num_stages"})
 
 
-class KernelConfig(Mapping[str, int]):
-    """An immutable, hashable set of integer tuning parameters for one operation."""
+def _canonical(params: Mapping[str, int]) -> str:
+    return json.dumps(dict(params), sort_keys=True, separators=(",", ":"))
 
-    __slots__ = ("operation", "_params")
+
+def _require_int(key: str, value: object) -> int:
+    # bool is an int subclass and numpy integers are not ints: both are refused,
+    # so a config always serialises to plain JSON integers.
+    if isinstance(value, bool) or not isinstance(value, int):
+        raise TypeError(f"config parameter {key!r} must be an int, got {value!r}")
+    return int(value)
+
+
+def _rebuild_config(operation: str, pairs: tuple[tuple[str, int], ...]) -> KernelConfig:
+    return KernelConfig(operation, **dict(pairs))
+
+
+class KernelConfig(Mapping[str, int]):
+    """Immutable, hashable, order-independent integer parameters of one operation.
+
+    Stored as a sorted tuple of pairs; the mapping view, the canonical JSON
+    and the digest are all derived from it, so two configs are equal exactly
+    when their digests are.
+    """
+
+    __slots__ = ("operation", "_pairs", "_index")
 
     def __init__(self, operation: str, **params: int) -> None:
-        for key, value in params.items():
-            if not isinstance(value, int) or isinstance(value, bool):
-                raise TypeError(f"config parameter {key!r} must be an int, got {value!r}")
-        self.operation = operation
-        self._params: dict[str, int] = {k: params[k] for k in sorted(params)}
+        pairs = tuple(sorted((k, _require_int(k, v)) for k, v in params.items()))
+        object.__setattr__(self, "operation", operation)
+        object.__setattr__(self, "_pairs", pairs)
+        object.__setattr__(self, "_index", dict(pairs))
 
+    def __setattr__(self, name: str, value: object) -> None:
+        raise AttributeError("KernelConfig is immutable; use with_params()")
+
+    def __reduce__(self):
+        return (_rebuild_config, (self.operation, self._pairs))
+
+    # Mapping protocol ------------------------------------------------------
     def __getitem__(self, key: str) -> int:
-        return self._params[key]
+        return self._index[key]
 
     def __iter__(self) -> Iterator[str]:
-        return iter(self._params)
+        return (k for k, _ in self._pairs)
 
     def __len__(self) -> int:
-        return len(self._params)
+        return len(self._pairs)
 
     def __hash__(self) -> int:
-        return hash((self.operation, tuple(self._params.items())))
+        return hash((self.operation, self._pairs))
 
     def __eq__(self, other: object) -> bool:
-        if not isinstance(other, KernelConfig):
-            return NotImplemented
-        return self.operation == other.operation and self._params == other._params
+        if isinstance(other, KernelConfig):
+            return (self.operation, self._pairs) == (other.operation, other._pairs)
+        return NotImplemented
 
     def __repr__(self) -> str:
-        body = ", ".join(f"{k}={v}" for k, v in self._params.items())
-        return f"KernelConfig({self.operation!r}, {body})"
+        inner = ", ".join(f"{k}={v}" for k, v in self._pairs)
+        return f"KernelConfig({self.operation!r}, {inner})"
+
+    # Views ------------------------------------------------------------------
+    def _split(self, launch: bool) -> dict[str, int]:
+        return {k: v for k, v in self._pairs if (k in LAUNCH_KEYS) == launch}
 
     @property
     def meta(self) -> dict[str, int]:
-        """Tile/instantiation parameters."""
-        return {k: v for k, v in self._params.items() if k not in LAUNCH_KEYS}
+        """Instantiation parameters: tile, pipeline, split and strip sizes."""
+        return self._split(launch=False)
 
     @property
     def launch(self) -> dict[str, int]:
-        """Launch-shape parameters (``num_warps`` / ``num_stages``)."""
-        return {k: v for k, v in self._params.items() if k in LAUNCH_KEYS}
+        """Launch parameters: ``num_warps`` (wave64 count) and ``num_stages``."""
+        return self._split(launch=True)
+
+    @property
+    def waves(self) -> int | None:
+        """Wavefronts per workgroup (``num_warps``), if the config sets it."""
+        return self._index.get("num_warps")
 
     def as_dict(self) -> dict[str, int]:
-        return dict(self._params)
+        return dict(self._pairs)
 
+    def with_params(self, **changes: int) -> KernelConfig:
+        """A copy with some parameters replaced or added."""
+        merged = dict(self._pairs)
+        merged.update(changes)
+        return KernelConfig(self.operation, **merged)
+
+    # Interchange --------------------------------------------------------------
     def to_json(self) -> str:
-        return json.dumps(self._params, sort_keys=True, separators=(",", ":"))
+        return _canonical(self._index)
 
     @property
     def digest(self) -> str:
-        """Short content hash: sha1 of ``operation|json``, first 16 hex digits."""
-        payload = f"{self.operation}|{self.to_json()}"
-        return hashlib.sha1(payload.encode()).hexdigest()[:16]
+        """Database identity: sha1 of ``operation|canonical json``, 16 hex digits."""
+        return hashlib.sha1(f"{self.operation}|{self.to_json()}".encode()).hexdigest()[:16]
 
     @classmethod
     def from_json(cls, operation: str, payload: str) -> KernelConfig:
         return cls(operation, **json.loads(payload))
 
+    @classmethod
+    def parse(cls, operation: str, text: str) -> KernelConfig:
+        """``"BLOCK_M=128,BLOCK_N=256,num_warps=8"`` (the CLI's --config form)."""
+        params: dict[str, int] = {}
+        for item in filter(None, (part.strip() for part in text.split(","))):
+            key, sep, value = item.partition("=")
+            if not sep:
+                raise ValueError(f"config item {item!r} is not KEY=VALUE")
+            params[key.strip()] = int(value)
+        return cls(operation, **params)
+
     def render(self, order: tuple[str, ...] = ()) -> str:
-        """Aligned multi-line rendering for CLI output."""
-        keys = [k for k in order if k in self._params]
-        keys += [k for k in self._params if k not in keys]
-        width = max((len(k) for k in keys), default=0)
-        return "\n".join(f"{k + ':':<{width + 1}} {self._params[k]:>4}" for k in keys)
+        """One ``KEY: value`` line per parameter, keys in ``order`` first, aligned."""
+        ranked = sorted(self._index, key=lambda k: (order.index(k) if k in order else len(order), k))
+        pad = 1 + max((len(k) for k in ranked), default=0)
+        return "\n".join(f"{(k + ':').ljust(pad)} {self._index[k]:>4}" for k in ranked)
 
 
-@dataclass(frozen=True)
 class Problem:
-    """One concrete workload: an operation at named dimensions and a dtype."""
+    """One workload: an operation over named dimensions in one dtype.
 
-    operation: str
-    dims: tuple[tuple[str, int], ...]
-    dtype: torch.dtype
+    Dimension names travel with the values (``M/N/K`` for products,
+    ``rows/cols`` for row kernels, ``n`` for elementwise) because they become
+    parts of cache keys and database rows.
+    """
+
+    __slots__ = ("operation", "dims", "dtype", "_key")
+
+    def __init__(self, operation: str, dims: tuple[tuple[str, int], ...], dtype: torch.dtype):
+        object.__setattr__(self, "operation", operation)
+        object.__setattr__(self, "dims", tuple((str(k), int(v)) for k, v in dims))
+        object.__setattr__(self, "dtype", dtype)
+        object.__setattr__(self, "_key", (operation, self.dims, dtype))
+
+    def __setattr__(self, name: str, value: object) -> None:
+        raise AttributeError("Problem is immutable")
+
+    def __reduce__(self):
+        return (Problem, (self.operation, self.dims, self.dtype))
 
     @classmethod
     def create(cls, operation: str, dtype: str | torch.dtype, **dims: int) -> Problem:
-        for key, value in dims.items():
-            if not isinstance(value, int) or isinstance(value, bool) or value < 1:
-                raise ValueError(f"dimension {key!r} must be a positive int, got {value!r}")
-        return cls(operation=operation, dims=tuple(dims.items()), dtype=parse_dtype(dtype))
+        bad = {k: v for k, v in dims.items() if isinstance(v, bool) or not isinstance(v, int) or v < 1}
+        if bad:
+            key, value = next(iter(bad.items()))
+            raise ValueError(f"dimension {key!r} must be a positive int, got {value!r}")
+        return cls(operation, tuple(dims.items()), parse_dtype(dtype))
+
+    def __eq__(self, other: object) -> bool:
+        if isinstance(other, Problem):
+            return self._key == other._key
+        return NotImplemented
+
+    def __hash__(self) -> int:
+        return hash(self._key)
+
+    def __repr__(self) -> str:
+        return f"Problem({self.cache_key})"
 
     def __getitem__(self, key: str) -> int:
-        return self.dims_dict[key]
+        for name, value in self.dims:
+            if name == key:
+                return value
+        raise KeyError(key)
 
     @property
     def dims_dict(self) -> dict[str, int]:
@@ -117,8 +206,8 @@ class Problem:
 
     @property
     def shape_key(self) -> str:
-        """Dimensions in declaration order, e.g. ``2048x4096x4096``."""
-        return "x".join(str(v) for _, v in self.dims)
+        """Values in declaration order: ``2048x4096x4096``."""
+        return "x".join(map(str, (v for _, v in self.dims)))
 
     @property
     def dtype_name(self) -> str:
@@ -130,17 +219,14 @@ class Problem:
 
     @property
     def cache_key(self) -> str:
-        return f"{self.operation}/{self.dtype_name}/{self.shape_key}"
+        return "/".join((self.operation, self.dtype_name, self.shape_key))
 
     def describe(self) -> str:
-        shape = " x ".join(f"{v}" for _, v in self.dims)
-        names = "/".join(k for k, _ in self.dims)
-        return f"{self.operation} {names}={shape} {self.dtype_name}"
+        """``matmul M/N/K=2048 x 4096 x 4096 fp16``."""
+        names = "/".join(name for name, _ in self.dims)
+        values = " x ".join(str(v) for _, v in self.dims)
+        return f"{self.operation} {names}={values} {self.dtype_name}"
 
     def as_dict(self) -> dict[str, Any]:
-        return {
-            "operation": self.operation,
-            "dims": self.dims_dict,
-            "dtype": self.dtype_name,
-            "shape_key": self.shape_key,
-        }
+        return {"operation": self.operation, "dims": self.dims_dict, "dtype": self.dtype_name,
+                "shape_key": self.shape_key}

@@ -35,7 +35,7 @@ def lib():
 
 def test_header_declares_the_expected_entry_points():
     assert _declared() == {
-        "kf_abi_version", "kf_build_target", "kf_last_error",
+        "kf_abi_version", "kf_build_target", "kf_last_error", "kf_stream_capture_id",
         "kf_gemm", "kf_gemm_has_variant", "kf_gemm_variant_count", "kf_gemm_variant_info",
         "kf_gemm_split_k", "kf_gemm_workspace_bytes", "kf_gemm_concurrent_tiles",
         "kf_gemv", "kf_gemv_workspace_bytes", "kf_softmax", "kf_rmsnorm",
@@ -51,7 +51,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_identification(lib):
-    assert lib.kf_abi_version() == hip.ABI_VERSION == 4
+    assert lib.kf_abi_version() == hip.ABI_VERSION == 5
     assert lib.kf_build_target() == b"gfx950"
 
 

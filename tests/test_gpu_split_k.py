@@ -255,3 +255,62 @@ def test_split_k_through_the_operator_and_a_graph():
             assert torch.equal(got, want)
         _ = run()
         torch.cuda.synchronize()
+
+
+def test_split_k_workspaces_of_captured_graphs_stay_private():
+    """Graphs keep the split-K workspace they were captured with.
+
+    Graph A captures a small split-K GEMV; graph B, captured later, a split-K
+    GEMM that needs a larger workspace. Eager calls that need a larger eager
+    workspace still run in between. Every replay of A and of B must equal the
+    eager result bit for bit: a graph replaying on a workspace that was freed
+    and handed to someone else, or whose counters another graph left non-zero,
+    would not."""
+    from kernelforge.kernels.matmul import launch_gemm
+
+    gemv_cfg = KernelConfig("matmul", GEMV=1, SPLIT_K=4, LANES_PER_ROW=16, num_warps=4)
+    gemm_cfg = KernelConfig("matmul", BLOCK_M=32, BLOCK_N=64, BLOCK_K=64, GROUP_M=8, DIRECT=1,
+                            SPLIT_K=8, num_warps=4, num_stages=3)
+    xa = _randn(1, 4096, dtype=torch.float16, seed=41).to(DEV)
+    wa = _randn(4096, 4096, dtype=torch.float16, seed=42, scale=1 / 64).to(DEV)
+    xb = _randn(64, 4096, dtype=torch.float16, seed=43).to(DEV)
+    wb = _randn(4096, 11008, dtype=torch.float16, seed=44, scale=1 / 64).to(DEV)
+
+    def run_a():
+        out = torch.empty(1, 4096, dtype=torch.float16, device=DEV)
+        launch_gemm(xa, wa, None, out, gemv_cfg)
+        return out
+
+    def run_b():
+        out = torch.empty(64, 11008, dtype=torch.float16, device=DEV)
+        launch_gemm(xb, wb, None, out, gemm_cfg)
+        return out
+
+    want_a, want_b = run_a(), run_b()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm up outside the capture, as torch.cuda.graph asks
+        run_a()
+        run_b()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph_a, graph_b = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph_a):
+        out_a = run_a()
+    with torch.cuda.graph(graph_b):
+        out_b = run_b()
+    torch.cuda.synchronize()
+    for rnd in range(3):
+        graph_a.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_a, want_a), f"replay {rnd} of graph A"
+        # An eager call that needs more workspace than any before it.
+        big = torch.empty(128, 11008, dtype=torch.float16, device=DEV)
+        launch_gemm(_randn(128, 4096, dtype=torch.float16, seed=45).to(DEV), wb, None, big,
+                    KernelConfig("matmul", BLOCK_M=32, BLOCK_N=64, BLOCK_K=64, GROUP_M=8,
+                                 DIRECT=1, SPLIT_K=16, num_warps=4, num_stages=3))
+        graph_b.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_b, want_b), f"replay {rnd} of graph B"
+        assert torch.equal(run_a(), want_a) and torch.equal(run_b(), want_b)
