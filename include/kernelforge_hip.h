@@ -192,6 +192,31 @@ int kf_gemv(int dtype, const void* x, const void* W, const void* bias, void* y,
             void* stream);
 size_t kf_gemv_workspace_bytes(int64_t M, int64_t N, int split_k);
 
+/* Size of the static scratch behind kf_gemv_no_alloc, per GPU: the
+ * KF_WORKSPACE_COUNTER_BYTES counter region plus 15 MiB of fp32 partials, so
+ * split_k * M * N <= 3,932,160 (e.g. M=8, N=11008, split_k=44). */
+enum { KF_GEMV_NO_ALLOC_SCRATCH_BYTES = 16 << 20 };
+
+/*
+ * kf_gemv without a workspace argument and without allocating: no hipMalloc,
+ * hipFree or allocating library call. No counterpart in the reference; it is
+ * for callers that cannot allocate (code under HIP graph capture, tight
+ * decode-serving loops, harnesses that forbid allocation). Same arguments,
+ * kernels, results and error codes as kf_gemv; the split-K workspace is a
+ * file-scope device array of KF_GEMV_NO_ALLOC_SCRATCH_BYTES that each GPU
+ * holds from its first call until the process ends. A split that needs more
+ * (kf_gemv_workspace_bytes(M, N, split_k) > KF_GEMV_NO_ALLOC_SCRATCH_BYTES)
+ * returns KF_ERR_WORKSPACE. The first call on a device also enqueues a
+ * kernel that zeroes the counters. Every call on one GPU shares its array:
+ * calls that overlap on one GPU (different streams, concurrent graph
+ * replays) race and must be serialised by the caller.
+ */
+int kf_gemv_no_alloc(int dtype, const void* x, const void* W, const void* bias, void* y,
+                     int64_t M, int64_t N, int64_t K,
+                     int64_t ldx_m, int64_t ldx_k, int64_t ldw_k, int64_t ldw_n,
+                     int64_t ldy_m, int64_t ldy_n, int epilogue,
+                     int split_k, int waves, int lanes_per_row, void* stream);
+
 /*
  * Single-pass row softmax over the last dimension, fp32 internal.
  * Replaces softmax() (kernels/softmax.py:70-104). Rows must have unit column

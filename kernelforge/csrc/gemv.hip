@@ -23,6 +23,7 @@
 // BLOCK_M=16 (kernels/matmul.py:54-113, tuning/search.py:377-386).
 #include <math.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -192,7 +193,6 @@ __global__ __launch_bounds__(gemv_max_lanes<MR>()) void gemv_splitk(
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int nwaves = blockDim.x / kWave;
-  const int nthreads = blockDim.x;
   const int sub = lane / LPR;                 // row of the wave load
   const int cv = (lane % LPR) * V;            // column of the lane's vector within the strip
   const int64_t nb = blockIdx.x;
@@ -542,12 +542,15 @@ extern "C" size_t kf_gemv_workspace_bytes(int64_t M, int64_t N, int split_k) {
          static_cast<size_t>(split_k) * M * N * sizeof(float);
 }
 
-extern "C" int kf_gemv(int dtype, const void* x, const void* W, const void* bias, void* y,
-                       int64_t M, int64_t N, int64_t K, int64_t ldx_m, int64_t ldx_k,
-                       int64_t ldw_k, int64_t ldw_n, int64_t ldy_m, int64_t ldy_n, int epilogue,
-                       int split_k, int waves, int lanes_per_row, void* workspace,
-                       size_t workspace_bytes, void* stream) {
-  using namespace kf;
+namespace kf {
+namespace {
+
+// Argument checks, workspace check and dispatch shared by kf_gemv and
+// kf_gemv_no_alloc; they differ only in where the workspace comes from.
+int gemv_entry(int dtype, const void* x, const void* W, const void* bias, void* y, int64_t M,
+               int64_t N, int64_t K, int64_t ldx_m, int64_t ldx_k, int64_t ldw_k, int64_t ldw_n,
+               int64_t ldy_m, int64_t ldy_n, int epilogue, int split_k, int waves,
+               int lanes_per_row, void* workspace, size_t workspace_bytes, void* stream) {
   if (M < 0 || N < 0 || K < 0) {
     set_error("gemv: negative shape");
     return KF_ERR_INVALID_ARGUMENT;
@@ -610,4 +613,109 @@ extern "C" int kf_gemv(int dtype, const void* x, const void* W, const void* bias
       set_error("gemv: unsupported dtype code %d", dtype);
       return KF_ERR_UNSUPPORTED_DTYPE;
   }
+}
+
+// ---------------------------------------------------------------------------
+// The no-allocation variant's workspace: one file-scope device array per GPU,
+// laid out like every split-K workspace (counters, then fp32 partials). In
+// host code `gemv_scratch` names a host-side stand-in, not device memory, so
+// it is only ever used through the address hipGetSymbolAddress returns for
+// the current device.
+static __device__ __align__(256) unsigned char gemv_scratch[KF_GEMV_NO_ALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+
+struct DeviceScratch {
+  void* ptr = nullptr;   // device address of gemv_scratch on this GPU
+  bool cleared = false;  // its counters were zeroed by an executed (not captured) launch
+};
+std::mutex g_scratch_mu;
+DeviceScratch g_scratch[kMaxDevices];
+
+// Zero the counter region: one 16-byte store per lane.
+__global__ __launch_bounds__(256) void clear_counters(u32x4* __restrict__ counters, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) counters[i] = u32x4{0u, 0u, 0u, 0u};
+}
+
+// Device address of the current GPU's scratch array. On the first call per
+// device the counters are zeroed by a kernel on `s` (a fill kernel, not a
+// memset, so a call under graph capture records an ordinary kernel node);
+// until such a launch has run outside a capture, every call enqueues it again.
+int gemv_scratch_for_current_device(hipStream_t s, void** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("gemv_no_alloc: no usable current device (%s, device %d)", hipGetErrorName(err), dev);
+    return KF_ERR_LAUNCH;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  DeviceScratch& d = g_scratch[dev];
+  if (d.ptr == nullptr) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(gemv_scratch));
+    if (err != hipSuccess || ptr == nullptr) {
+      set_error("gemv_no_alloc: hipGetSymbolAddress of the scratch array failed on device %d: %s",
+                dev, hipGetErrorName(err));
+      return KF_ERR_LAUNCH;
+    }
+    d.ptr = ptr;
+  }
+  if (!d.cleared) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    err = hipStreamIsCapturing(s, &capture);
+    if (err != hipSuccess) {
+      set_error("gemv_no_alloc: hipStreamIsCapturing failed: %s", hipGetErrorName(err));
+      return KF_ERR_LAUNCH;
+    }
+    constexpr int n = KF_WORKSPACE_COUNTER_BYTES / 16;
+    hipLaunchKernelGGL(clear_counters, dim3(n / 256), dim3(256), 0, s,
+                       static_cast<u32x4*>(d.ptr), n);
+    const int rc = launch_status("gemv_no_alloc: counter clear");
+    if (rc != KF_OK) return rc;
+    if (capture == hipStreamCaptureStatusNone) d.cleared = true;
+  }
+  *out = d.ptr;
+  return KF_OK;
+}
+
+}  // namespace
+}  // namespace kf
+
+extern "C" int kf_gemv(int dtype, const void* x, const void* W, const void* bias, void* y,
+                       int64_t M, int64_t N, int64_t K, int64_t ldx_m, int64_t ldx_k,
+                       int64_t ldw_k, int64_t ldw_n, int64_t ldy_m, int64_t ldy_n, int epilogue,
+                       int split_k, int waves, int lanes_per_row, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  return kf::gemv_entry(dtype, x, W, bias, y, M, N, K, ldx_m, ldx_k, ldw_k, ldw_n, ldy_m, ldy_n,
+                        epilogue, split_k, waves, lanes_per_row, workspace, workspace_bytes,
+                        stream);
+}
+
+extern "C" int kf_gemv_no_alloc(int dtype, const void* x, const void* W, const void* bias,
+                                void* y, int64_t M, int64_t N, int64_t K, int64_t ldx_m,
+                                int64_t ldx_k, int64_t ldw_k, int64_t ldw_n, int64_t ldy_m,
+                                int64_t ldy_n, int epilogue, int split_k, int waves,
+                                int lanes_per_row, void* stream) {
+  using namespace kf;
+  // Shapes kf_gemv rejects, and zero-size calls, go straight to its checks
+  // without touching the scratch array.
+  const bool needs_scratch = split_k > 1 && split_k <= 65535 && M >= 1 && M <= 8 && N >= 1 &&
+                             K >= 0;
+  if (!needs_scratch)
+    return gemv_entry(dtype, x, W, bias, y, M, N, K, ldx_m, ldx_k, ldw_k, ldw_n, ldy_m, ldy_n,
+                      epilogue, split_k, waves, lanes_per_row, nullptr, 0, stream);
+  const size_t need = kf_gemv_workspace_bytes(M, N, split_k);
+  if (need > static_cast<size_t>(KF_GEMV_NO_ALLOC_SCRATCH_BYTES) || N > KF_WORKSPACE_COUNTERS) {
+    set_error("gemv_no_alloc: split_k=%d over %lldx%lld outputs needs %zu bytes of workspace, "
+              "more than the %d bytes of static scratch; use kf_gemv with a workspace",
+              split_k, (long long)M, (long long)N, need, KF_GEMV_NO_ALLOC_SCRATCH_BYTES);
+    return KF_ERR_WORKSPACE;
+  }
+  void* scratch = nullptr;
+  const int rc = gemv_scratch_for_current_device(static_cast<hipStream_t>(stream), &scratch);
+  if (rc != KF_OK) return rc;
+  return gemv_entry(dtype, x, W, bias, y, M, N, K, ldx_m, ldx_k, ldw_k, ldw_n, ldy_m, ldy_n,
+                    epilogue, split_k, waves, lanes_per_row, scratch,
+                    static_cast<size_t>(KF_GEMV_NO_ALLOC_SCRATCH_BYTES), stream);
 }

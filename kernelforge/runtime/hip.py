@@ -37,6 +37,7 @@ KF_PIPELINE_STAGED = 0
 KF_PIPELINE_DIRECT = 1
 
 KF_WORKSPACE_COUNTER_BYTES = 4 << 18
+KF_GEMV_NO_ALLOC_SCRATCH_BYTES = 16 << 20
 
 
 class KernelError(RuntimeError):
@@ -115,6 +116,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _int, _int, _int, _vp, _sz, _vp],
     ),
     "kf_gemv_workspace_bytes": (_sz, [_i64, _i64, _int]),
+    "kf_gemv_no_alloc": (
+        _int,
+        [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int,
+         _int, _int, _int, _vp],
+    ),
     "kf_gemm_split_k": (
         _int,
         [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int,

@@ -38,7 +38,7 @@ def test_header_declares_the_expected_entry_points():
         "kf_abi_version", "kf_build_target", "kf_last_error", "kf_stream_capture_id",
         "kf_gemm", "kf_gemm_has_variant", "kf_gemm_variant_count", "kf_gemm_variant_info",
         "kf_gemm_split_k", "kf_gemm_workspace_bytes", "kf_gemm_concurrent_tiles",
-        "kf_gemv", "kf_gemv_workspace_bytes", "kf_softmax", "kf_rmsnorm",
+        "kf_gemv", "kf_gemv_workspace_bytes", "kf_gemv_no_alloc", "kf_softmax", "kf_rmsnorm",
         "kf_rmsnorm_two_pass", "kf_rmsnorm_two_pass_max_staged_cols", "kf_vector_add",
     }
 
@@ -186,6 +186,34 @@ def test_gemv_argument_errors(lib):
     rc, msg = _rc_and_message(lambda: gemv(epi=1))
     assert rc == hip.KF_ERR_INVALID_ARGUMENT
     assert gemv(m=0) == hip.KF_OK
+
+
+def test_gemv_no_alloc_argument_errors(lib):
+    """kf_gemv_no_alloc: kf_gemv's checks, plus the static scratch limit.
+
+    Every case here returns before the library asks the runtime for anything
+    (no device, no launch), so it runs without a GPU.
+    """
+
+    def gemv(m=1, n=64, k=64, split=1, waves=4, dtype=2, epi=0, lanes=16):
+        return lib.kf_gemv_no_alloc(dtype, 1 << 20, 1 << 20, NULL, 1 << 20, m, n, k, k, 1, n, 1,
+                                    n, 1, epi, split, waves, lanes, NULL)
+
+    rc, msg = _rc_and_message(lambda: gemv(m=9, split=4))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "decode limit" in msg
+    rc, msg = _rc_and_message(lambda: gemv(split=0))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "split_k" in msg
+    rc, msg = _rc_and_message(lambda: gemv(lanes=12))
+    assert rc == hip.KF_ERR_INVALID_ARGUMENT and "lanes_per_row" in msg
+    # The largest split the scratch holds, and one beyond it.
+    limit = hip.KF_GEMV_NO_ALLOC_SCRATCH_BYTES - hip.KF_WORKSPACE_COUNTER_BYTES
+    n = 11008
+    fits = limit // (8 * n * 4)
+    assert lib.kf_gemv_workspace_bytes(8, n, fits) <= hip.KF_GEMV_NO_ALLOC_SCRATCH_BYTES
+    rc, msg = _rc_and_message(lambda: gemv(m=8, n=n, split=fits + 1))
+    assert rc == hip.KF_ERR_WORKSPACE and "static scratch" in msg and str(hip.KF_GEMV_NO_ALLOC_SCRATCH_BYTES) in msg
+    # Zero-size calls return without touching the scratch.
+    assert gemv(m=0, split=4) == hip.KF_OK and gemv(n=0, split=4) == hip.KF_OK
 
 
 def test_row_kernel_argument_errors(lib):
