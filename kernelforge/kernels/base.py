@@ -66,6 +66,16 @@ class Operator(ABC):
         """
         return {"torch_eager": lambda: self.reference(*inputs)}
 
+    def availability(self, config: KernelConfig, problem: Problem) -> str:
+        """Why ``config`` cannot run for ``problem`` in this build, or ``""``.
+
+        Kernels are compiled ahead of time, so an operator can answer from
+        the library's variant table without launching anything; the tuner
+        records a non-empty answer as a compile error. The default claims
+        every configuration is available and lets the launch decide.
+        """
+        return ""
+
     def is_memory_bound(self) -> bool:
         """Whether GB/s (True) or TFLOP/s (False) is the headline metric."""
         return False

@@ -90,6 +90,11 @@ class FusedLinearOperator(Operator):
         x, w, bias = inputs
         return linear_gelu_reference(x, w, bias)
 
+    def availability(self, config: KernelConfig, problem: Problem) -> str:
+        from kernelforge.kernels.matmul import gemm_availability
+
+        return gemm_availability(config, problem.dtype)
+
     def run(self, config: KernelConfig, *inputs: torch.Tensor) -> torch.Tensor:
         x, w, bias = inputs
         return fused_linear_gelu(x, w, bias, config=config)

@@ -112,6 +112,26 @@ def launch_gemm(
     return out
 
 
+def gemm_availability(cfg: KernelConfig, dtype: torch.dtype) -> str:
+    """Why the library cannot run ``cfg`` (tile family, pipeline) in ``dtype``, or ``""``.
+
+    GEMV configurations select a kernel by template arguments that every
+    build contains; tile configurations are looked up in the variant table.
+    """
+    if cfg.get("GEMV"):
+        return ""
+    direct = bool(cfg.get("DIRECT"))
+    found = hip.load().kf_gemm_has_variant(
+        abi_code(dtype), cfg["BLOCK_M"], cfg["BLOCK_N"], cfg["BLOCK_K"], cfg["num_warps"],
+        cfg.get("num_stages", 2),
+        hip.KF_PIPELINE_DIRECT if direct else hip.KF_PIPELINE_STAGED)
+    if found:
+        return ""
+    return (f"no ahead-of-time instantiation of {cfg['BLOCK_M']}x{cfg['BLOCK_N']}x"
+            f"{cfg['BLOCK_K']} with {cfg['num_warps']} waves, {cfg.get('num_stages', 2)} stages on "
+            f"the {'direct' if direct else 'staged'} pipeline for {dtype}")
+
+
 def matmul(a: torch.Tensor, b: torch.Tensor, *, config: KernelConfig | None = None) -> torch.Tensor:
     _check_operands(a, b)
     m, k = a.shape
@@ -153,6 +173,9 @@ class MatmulOperator(Operator):
     def default_config(self, problem: Problem) -> KernelConfig:
         d = problem.dims_dict
         return _heuristic_config("matmul", d["M"], d["N"], d["K"], problem.dtype)
+
+    def availability(self, config: KernelConfig, problem: Problem) -> str:
+        return gemm_availability(config, problem.dtype)
 
     def flops(self, problem: Problem) -> int:
         d = problem.dims_dict

@@ -1,14 +1,18 @@
-"""Correctness gate.
+"""The correctness gate every tuning candidate passes before it is timed.
 
-Every tuning candidate passes :func:`verify` before it may be timed, so an
-incorrect configuration is never ranked. The metric is the reference's
-scale-invariant normalised infinity norm (kernelforge/testing.py:64-139),
+Semantics are the reference's (kernelforge/testing.py:26-175), because they
+define parity:
 
-    err = max|out - ref| / max|ref|
+    error = max|out - ref| / max|ref|       (max|out - ref| when ref is all zero)
 
-with one threshold per dtype (fp32 1e-5, fp16 5e-3, bf16 2e-2), falling back
-to the absolute error for an all-zero reference. Shape mismatch and
-non-finite output fail with ``inf``; an empty tensor passes.
+passes at or below one threshold per dtype -- fp32 1e-5, fp16 5e-3,
+bf16 2e-2. A shape mismatch or any non-finite output fails with an infinite
+error; an empty tensor passes. The comparison runs in fp32.
+
+The implementation is built for a device-resident output: every statistic the
+verdict needs (non-finite count, largest difference, reference scale, and the
+count of elements beyond the budget) is reduced on the output's device and
+fetched with one host synchronisation, instead of one per statistic.
 """
 
 from __future__ import annotations
@@ -36,19 +40,65 @@ class VerificationResult:
     reason: str = ""
 
     def __str__(self) -> str:
-        if self.passed:
-            return f"ok (err={self.error:.3e} <= {self.threshold:.1e})"
-        return f"FAIL ({self.reason})"
+        if not self.passed:
+            return f"FAIL ({self.reason})"
+        return f"ok (err={self.error:.3e} <= {self.threshold:.1e})"
 
 
 def threshold_for(dtype: torch.dtype) -> float:
-    try:
+    if dtype in ERROR_THRESHOLDS:
         return ERROR_THRESHOLDS[dtype]
-    except KeyError:
-        raise ValueError(
-            f"no correctness threshold defined for {dtype}; "
-            f"known dtypes: {sorted(str(d) for d in ERROR_THRESHOLDS)}"
-        ) from None
+    known = sorted(str(d) for d in ERROR_THRESHOLDS)
+    raise ValueError(f"no correctness threshold defined for {dtype}; known dtypes: {known}")
+
+
+class Gate:
+    """A normalised infinity-norm check at one threshold."""
+
+    def __init__(self, threshold: float) -> None:
+        self.threshold = float(threshold)
+
+    @classmethod
+    def for_dtype(cls, dtype: torch.dtype) -> Gate:
+        return cls(threshold_for(dtype))
+
+    def _fail(self, total: int, bad: int, reason: str) -> VerificationResult:
+        inf = float("inf")
+        return VerificationResult(False, inf, inf, bad, total, self.threshold, reason)
+
+    def check(self, reference: torch.Tensor, output: torch.Tensor) -> VerificationResult:
+        total = output.numel()
+        if tuple(reference.shape) != tuple(output.shape):
+            return self._fail(total, total, f"shape mismatch: reference {tuple(reference.shape)} "
+                                            f"vs output {tuple(output.shape)}")
+        if total == 0:
+            return VerificationResult(True, 0.0, 0.0, 0, 0, self.threshold)
+
+        out = output.detach().float()
+        ref = reference.detach().to(device=out.device, dtype=torch.float32)
+        diff = (out - ref).abs()
+        scale = ref.abs().max()
+        # Elements beyond the same bound the verdict uses, so a failing check
+        # never reports that nothing differs.
+        budget = torch.where(scale > 0, scale * self.threshold,
+                             torch.full_like(scale, self.threshold))
+        stats = torch.stack([
+            (~torch.isfinite(out)).sum().float(),
+            diff.max(),
+            scale,
+            (diff > budget).sum().float(),
+        ]).tolist()  # the one synchronisation
+        non_finite, max_abs, ref_scale, beyond = stats
+        if non_finite:
+            bad = int(non_finite)
+            return self._fail(total, bad, f"output contains {bad}/{total} non-finite values")
+        error = max_abs / ref_scale if ref_scale > 0 else max_abs
+        ok = error <= self.threshold
+        reason = "" if ok else (
+            f"normalised error {error:.3e} exceeds {self.threshold:.1e} "
+            f"(max|diff|={max_abs:.3e}, {int(beyond)}/{total} elements off)"
+        )
+        return VerificationResult(ok, error, max_abs, int(beyond), total, self.threshold, reason)
 
 
 def verify(
@@ -58,71 +108,14 @@ def verify(
     dtype: torch.dtype | None = None,
     threshold: float | None = None,
 ) -> VerificationResult:
-    """Compare a kernel output against a reference.
+    """Gate ``output`` against ``reference``.
 
-    ``dtype`` selects the threshold and defaults to the output dtype. The
-    comparison itself runs in fp32 on the output's device; a reference on
-    another device is moved there.
+    ``dtype`` picks the threshold (default: the output's dtype); pass it when
+    the reference was computed at higher precision than the kernel. The
+    reference may live on another device; it is moved to the output's.
     """
-    gate_dtype = dtype if dtype is not None else output.dtype
-    limit = threshold if threshold is not None else threshold_for(gate_dtype)
-
-    if tuple(reference.shape) != tuple(output.shape):
-        return VerificationResult(
-            passed=False,
-            error=float("inf"),
-            max_abs_err=float("inf"),
-            mismatched=output.numel(),
-            total=output.numel(),
-            threshold=limit,
-            reason=(
-                f"shape mismatch: reference {tuple(reference.shape)} vs output "
-                f"{tuple(output.shape)}"
-            ),
-        )
-
-    out = output.detach().to(torch.float32)
-    ref = reference.detach().to(device=out.device, dtype=torch.float32)
-    total = out.numel()
-    if total == 0:
-        return VerificationResult(True, 0.0, 0.0, 0, 0, limit)
-
-    finite = torch.isfinite(out)
-    if not bool(finite.all()):
-        n_bad = int((~finite).sum())
-        return VerificationResult(
-            passed=False,
-            error=float("inf"),
-            max_abs_err=float("inf"),
-            mismatched=n_bad,
-            total=total,
-            threshold=limit,
-            reason=f"output contains {n_bad}/{total} non-finite values",
-        )
-
-    diff = (out - ref).abs()
-    max_abs_err = float(diff.max())
-    scale = float(ref.abs().max())
-    error = max_abs_err / scale if scale > 0 else max_abs_err
-    passed = error <= limit
-    budget = limit * scale if scale > 0 else limit
-    mismatched = int((diff > budget).sum())
-    return VerificationResult(
-        passed=passed,
-        error=error,
-        max_abs_err=max_abs_err,
-        mismatched=mismatched,
-        total=total,
-        threshold=limit,
-        reason=(
-            ""
-            if passed
-            else (
-                f"normalised error {error:.3e} exceeds {limit:.1e} "
-                f"(max|diff|={max_abs_err:.3e}, {mismatched}/{total} elements off)"
-            )
-        ),
-    )
+    gate = Gate(threshold) if threshold is not None else Gate.for_dtype(dtype or output.dtype)
+    return gate.check(reference, output)
 
 
 def assert_verified(
@@ -133,30 +126,29 @@ def assert_verified(
     threshold: float | None = None,
     context: str = "",
 ) -> VerificationResult:
+    """:func:`verify`, raising ``AssertionError`` (prefixed by ``context``) on failure."""
     result = verify(reference, output, dtype=dtype, threshold=threshold)
-    if not result.passed:
-        prefix = f"{context}: " if context else ""
-        raise AssertionError(f"{prefix}{result.reason}")
-    return result
+    if result.passed:
+        return result
+    raise AssertionError(f"{context}: {result.reason}" if context else result.reason)
 
 
 @contextlib.contextmanager
 def exact_fp32_matmul():
-    """Disable reduced-precision fp32 matmuls for the duration of the block.
+    """Run fp32 matmuls at full fp32 precision inside the block.
 
-    An fp32 reference must be computed at full fp32 precision or it is the
-    least accurate number in the comparison (testing.py:157-175). On ROCm the
-    same torch flags govern hipBLASLt's TF32/XF32 paths; the CPU ignores them.
+    A reduced-precision (TF32/XF32) fp32 product carries about 1e-3 relative
+    error, a hundred times the fp32 threshold, so an fp32 reference computed
+    that way would be the least accurate number in the comparison. On ROCm
+    the same torch switches govern hipBLASLt; on the CPU they are inert.
     """
-    prev_matmul = torch.backends.cuda.matmul.allow_tf32
-    prev_cudnn = torch.backends.cudnn.allow_tf32
-    prev_precision = torch.get_float32_matmul_precision()
+    saved = (torch.backends.cuda.matmul.allow_tf32, torch.backends.cudnn.allow_tf32,
+             torch.get_float32_matmul_precision())
     torch.backends.cuda.matmul.allow_tf32 = False
     torch.backends.cudnn.allow_tf32 = False
     torch.set_float32_matmul_precision("highest")
     try:
         yield
     finally:
-        torch.backends.cuda.matmul.allow_tf32 = prev_matmul
-        torch.backends.cudnn.allow_tf32 = prev_cudnn
-        torch.set_float32_matmul_precision(prev_precision)
+        torch.backends.cuda.matmul.allow_tf32, torch.backends.cudnn.allow_tf32 = saved[:2]
+        torch.set_float32_matmul_precision(saved[2])

@@ -1,62 +1,94 @@
-"""The tuner: candidates -> filters -> verify -> time -> rank -> persist.
+"""Tune one problem: candidates -> availability -> gate -> time -> rank -> persist.
 
-Semantics kept from the reference (kernelforge/tuning/tuner.py:1-370):
+The guarantees are the reference's (kernelforge/tuning/tuner.py:1-370):
 
-* **An incorrect configuration is never ranked.** Every candidate runs once
-  and passes the gate before any timing; a failure is recorded with its
-  reason and dropped.
-* **Verification and timing are separate passes**, so no candidate's set-up
-  (here: first-launch LDS grants and code-object loading) lands inside
-  another candidate's measurement.
-* Failures are data: exceptions are classified by class name into
-  ``compile_error`` / ``out_of_memory`` / ``runtime_error``, a gate failure
-  is ``incorrect``, and every outcome becomes a database row.
+* **Nothing incorrect is ranked.** Every candidate passes the correctness gate
+  (:mod:`kernelforge.testing`) before it may be timed; a wrong answer is
+  recorded with its error and never timed.
+* **Gating and timing are separate passes.** All candidates are gated first,
+  then the survivors are timed back to back under identical settings, so no
+  candidate's timing shares the GPU with another candidate's setup.
+* **Ranking is on the median**, and failures are classified, recorded and
+  kept out of the ranking.
 
-On gfx950 "compile" means "has an ahead-of-time instantiation": a grid point
-without one raises :class:`~kernelforge.runtime.hip.KernelNotCompiled` and is
-recorded as a compile error, never silently skipped.
+How this build differs from a JIT tuner. Every configuration here is an
+ahead-of-time instantiation in ``libkernelforge_hip.so``. An operator can
+therefore say *before launching* whether a candidate exists
+(:meth:`Operator.availability`, backed by the library's variant table); a
+missing one is recorded as ``compile_error`` without touching the GPU. A
+launch that fails returns a ``KF_ERR_*`` status that the binding raises as a
+typed exception carrying the code, and the code decides the outcome:
+
+=========================================  ================
+``KF_ERR_NOT_BUILT``, ``KF_ERR_OUT_OF_RESOURCES``  ``compile_error``
+``KF_ERR_OUT_OF_MEMORY``                     ``out_of_memory``
+any other code                               ``runtime_error``
+=========================================  ================
+
+Exceptions from elsewhere (torch, a Python operator) have no code and fall
+back to the reference's rule on the class name: ``...OutOfMemory...`` is an
+OOM, ``...OutOfResources...``/``...Compil...``/``...Resource...`` a compile
+error, anything else a runtime error.
+
+Each candidate moves through the pipeline as a mutable :class:`_Trial`; the
+result exposes frozen :class:`CandidateOutcome` records.
 """
 
 from __future__ import annotations
 
 import time
+from collections import Counter
 from collections.abc import Callable
 from dataclasses import dataclass, field
 
 import torch
 
 from kernelforge.benchmark import metrics
-from kernelforge.benchmark.runner import (
-    DEFAULT_ITERATIONS,
-    DEFAULT_WARMUP,
-    TimingResult,
-    benchmark,
-)
+from kernelforge.benchmark.runner import DEFAULT_ITERATIONS, DEFAULT_WARMUP, TimingResult, benchmark
 from kernelforge.db import Measurement, ResultsDB
 from kernelforge.kernels.base import Operator
+from kernelforge.runtime import hip
 from kernelforge.runtime.env import Environment, capture_environment, device_caps, require_gpu
 from kernelforge.testing import VerificationResult, exact_fp32_matmul, verify
 from kernelforge.tuning.cache import ConfigCache
 from kernelforge.tuning.config import KernelConfig, Problem
 
+#: Candidate outcomes; only ``ok`` is ranked.
 STATUS_OK = "ok"
 STATUS_COMPILE_ERROR = "compile_error"
 STATUS_RUNTIME_ERROR = "runtime_error"
 STATUS_INCORRECT = "incorrect"
 STATUS_OOM = "out_of_memory"
 
-_MAX_ERROR_CHARS = 400
+#: The label tuned candidates carry in the results database.
+TUNED_LABEL = "kernelforge"
+
+_ERROR_CHARS = 400
+
+_BY_CODE = {
+    hip.KF_ERR_NOT_BUILT: STATUS_COMPILE_ERROR,
+    hip.KF_ERR_OUT_OF_RESOURCES: STATUS_COMPILE_ERROR,
+    hip.KF_ERR_OUT_OF_MEMORY: STATUS_OOM,
+}
+
+
+def _status_by_name(name: str) -> str:
+    if "OutOfMemory" in name:
+        return STATUS_OOM
+    if any(tag in name for tag in ("OutOfResources", "Compil", "Resource")):
+        return STATUS_COMPILE_ERROR
+    return STATUS_RUNTIME_ERROR
 
 
 def _classify(exc: BaseException) -> tuple[str, str]:
-    """Status and short message for an exception raised by a candidate."""
+    """(status, one-line message) for an exception a candidate raised."""
     name = type(exc).__name__
-    message = " ".join(str(exc).split())[:_MAX_ERROR_CHARS]
-    if "OutOfMemory" in name:
-        return STATUS_OOM, message
-    if "OutOfResources" in name or "Compil" in name or "Resource" in name:
-        return STATUS_COMPILE_ERROR, f"{name}: {message}"
-    return STATUS_RUNTIME_ERROR, f"{name}: {message}"
+    text = " ".join(str(exc).split())[:_ERROR_CHARS]
+    if isinstance(exc, hip.KernelError) and exc.code:
+        status = _BY_CODE.get(exc.code, STATUS_RUNTIME_ERROR)
+    else:
+        status = _status_by_name(name)
+    return status, (text if status == STATUS_OOM else f"{name}: {text}")
 
 
 @dataclass(frozen=True)
@@ -79,6 +111,24 @@ class CandidateOutcome:
 
 
 @dataclass
+class _Trial:
+    """One candidate on its way through the pipeline."""
+
+    config: KernelConfig
+    status: str = STATUS_OK
+    verification: VerificationResult | None = None
+    timing: TimingResult | None = None
+    error: str = ""
+
+    def fail(self, status: str, error: str) -> None:
+        self.status, self.error, self.timing = status, error, None
+
+    def freeze(self) -> CandidateOutcome:
+        return CandidateOutcome(self.config, self.status, self.verification, self.timing,
+                                self.error)
+
+
+@dataclass
 class TuningResult:
     problem: Problem
     environment: Environment
@@ -94,27 +144,25 @@ class TuningResult:
 
     @property
     def tested(self) -> int:
+        """Candidates that reached the gate (available ones plus AOT misses)."""
         return len(self.outcomes)
 
     @property
     def correct(self) -> int:
-        return sum(1 for o in self.outcomes if o.ok)
+        return sum(o.ok for o in self.outcomes)
 
     def ranked(self) -> list[CandidateOutcome]:
-        """Correct, timed candidates, fastest median first."""
-        return sorted(
-            (o for o in self.outcomes if o.ok and o.timing is not None), key=lambda o: o.median_ms
-        )
+        """Correct candidates by median latency, fastest first (never by the minimum,
+        which rewards the luckiest sample)."""
+        return sorted(filter(lambda o: o.ok, self.outcomes), key=lambda o: o.median_ms)
 
     @property
     def best(self) -> CandidateOutcome | None:
-        ranked = self.ranked()
-        return ranked[0] if ranked else None
+        return next(iter(self.ranked()), None)
 
     @property
     def best_config(self) -> KernelConfig | None:
-        best = self.best
-        return best.config if best else None
+        return None if self.best is None else self.best.config
 
     def tflops(self, ms: float) -> float:
         return metrics.tflops(self.flops, ms)
@@ -123,20 +171,17 @@ class TuningResult:
         return metrics.gbps(self.bytes_moved, ms)
 
     def speedup_over(self, label: str) -> float | None:
-        best = self.best
-        if best is None or label not in self.baselines:
+        base, best = self.baselines.get(label), self.best
+        if base is None or best is None:
             return None
-        return metrics.speedup(self.baselines[label].median_ms, best.median_ms)
+        return metrics.speedup(base.median_ms, best.median_ms)
 
     def status_counts(self) -> dict[str, int]:
-        counts: dict[str, int] = {}
-        for o in self.outcomes:
-            counts[o.status] = counts.get(o.status, 0) + 1
-        return counts
+        return dict(Counter(o.status for o in self.outcomes))
 
 
 class Tuner:
-    """Drives the pipeline for any :class:`Operator`."""
+    """Runs the pipeline for any :class:`~kernelforge.kernels.base.Operator`."""
 
     def __init__(
         self,
@@ -159,180 +204,121 @@ class Tuner:
         self.seed = seed
         self.db = db
         self.cache = cache
-        self._log = log
+        self._sink = log
 
     def log(self, message: str) -> None:
-        if self._log is not None:
-            self._log(message)
+        if self._sink is not None:
+            self._sink(message)
 
-    def tune(
-        self, operator: Operator, problem: Problem, *, device: torch.device | str | None = None
-    ) -> TuningResult:
-        started = time.perf_counter()
-        resolved = torch.device(device) if device is not None else require_gpu()
-        env = capture_environment(resolved if resolved.type == "cuda" else None)
-        caps = device_caps(resolved if resolved.type == "cuda" else None)
+    def _time(self, fn: Callable[[], object], device: torch.device) -> TimingResult:
+        return benchmark(fn, warmup=self.warmup, iterations=self.iterations, device=device,
+                         flush_l2=self.flush_l2)
 
-        candidates = operator.search_space().generate(
-            problem, caps, max_candidates=self.max_candidates
-        )
-        inputs = operator.make_inputs(problem, resolved, seed=self.seed)
-
+    # --- the pipeline -----------------------------------------------------------------
+    def tune(self, operator: Operator, problem: Problem, *,
+             device: torch.device | str | None = None) -> TuningResult:
+        began = time.perf_counter()
+        dev = torch.device(device) if device is not None else require_gpu()
+        env = capture_environment(dev)
+        plan = operator.search_space().generate(problem, device_caps(dev),
+                                                max_candidates=self.max_candidates)
+        trials = [_Trial(config) for config in plan]
+        inputs = operator.make_inputs(problem, dev, seed=self.seed)
+        # One numerical policy for candidates and baselines alike: fp32
+        # references and torch baselines at full fp32 precision.
         with exact_fp32_matmul():
             reference = operator.reference(*inputs)
-            self.log(f"Verifying candidates... ({len(candidates)} to check)")
-            outcomes = [
-                self._verify_candidate(operator, config, inputs, reference, problem)
-                for config in candidates
-            ]
-            passed = sum(1 for o in outcomes if o.ok)
-            self.log(f"{passed} / {len(candidates)} configurations passed correctness")
+            self.log(f"Verifying candidates... ({len(trials)} to check)")
+            for trial in trials:
+                self._gate(operator, problem, trial, inputs, reference)
+            self.log(f"{sum(t.status == STATUS_OK for t in trials)} / {len(trials)} "
+                     "configurations passed correctness")
             self.log("Benchmarking...")
-            timed = [self._time_candidate(operator, o, inputs, resolved) for o in outcomes]
-            baselines = (
-                self._measure_baselines(operator, problem, inputs, reference, resolved)
-                if self.measure_baselines
-                else {}
-            )
-
+            for trial in trials:
+                if trial.status == STATUS_OK:
+                    self._measure(operator, trial, inputs, dev)
+            baselines = (self._baselines(operator, problem, inputs, reference, dev)
+                         if self.measure_baselines else {})
         result = TuningResult(
             problem=problem,
             environment=env,
-            generated=candidates.generated,
-            feasible=candidates.feasible,
-            outcomes=tuple(timed),
+            generated=plan.generated,
+            feasible=plan.feasible,
+            outcomes=tuple(t.freeze() for t in trials),
             baselines=baselines,
             flops=operator.flops(problem),
             bytes_moved=operator.bytes_moved(problem),
-            elapsed_s=time.perf_counter() - started,
+            elapsed_s=time.perf_counter() - began,
             memory_bound=operator.is_memory_bound(),
-            rejections=candidates.rejected,
+            rejections=plan.rejected,
         )
-        self._persist(result, env)
+        self._store_winner(result)
+        self._record(result)
         return result
 
-    # --- stages -------------------------------------------------------------------
-    def _verify_candidate(
-        self,
-        operator: Operator,
-        config: KernelConfig,
-        inputs: tuple[torch.Tensor, ...],
-        reference: torch.Tensor,
-        problem: Problem,
-    ) -> CandidateOutcome:
+    def _gate(self, operator: Operator, problem: Problem, trial: _Trial,
+              inputs: tuple[torch.Tensor, ...], reference: torch.Tensor) -> None:
+        missing = operator.availability(trial.config, problem)
+        if missing:
+            trial.fail(STATUS_COMPILE_ERROR, missing)
+            return
         try:
-            output = operator.run(config, *inputs)
-        except Exception as exc:  # one failing candidate must not stop the sweep
-            status, message = _classify(exc)
-            return CandidateOutcome(config=config, status=status, error=message)
-        check = verify(reference, output, dtype=problem.dtype)
-        return CandidateOutcome(
-            config=config,
-            status=STATUS_OK if check.passed else STATUS_INCORRECT,
-            verification=check,
-            error="" if check.passed else check.reason,
-        )
+            output = operator.run(trial.config, *inputs)
+        except Exception as exc:  # one bad candidate must not end the sweep
+            trial.fail(*_classify(exc))
+            return
+        trial.verification = verify(reference, output, dtype=problem.dtype)
+        if not trial.verification.passed:
+            trial.fail(STATUS_INCORRECT, trial.verification.reason)
 
-    def _time_candidate(
-        self,
-        operator: Operator,
-        outcome: CandidateOutcome,
-        inputs: tuple[torch.Tensor, ...],
-        device: torch.device,
-    ) -> CandidateOutcome:
-        if not outcome.ok:
-            return outcome
+    def _measure(self, operator: Operator, trial: _Trial, inputs: tuple[torch.Tensor, ...],
+                 device: torch.device) -> None:
         try:
-            timing = benchmark(
-                lambda: operator.run(outcome.config, *inputs),
-                warmup=self.warmup,
-                iterations=self.iterations,
-                device=device,
-                flush_l2=self.flush_l2,
-            )
+            trial.timing = self._time(lambda: operator.run(trial.config, *inputs), device)
         except Exception as exc:
-            status, message = _classify(exc)
-            return CandidateOutcome(
-                config=outcome.config,
-                status=status,
-                verification=outcome.verification,
-                error=message,
-            )
-        return CandidateOutcome(
-            config=outcome.config,
-            status=STATUS_OK,
-            verification=outcome.verification,
-            timing=timing,
-        )
+            trial.fail(*_classify(exc))
 
-    def _measure_baselines(
-        self,
-        operator: Operator,
-        problem: Problem,
-        inputs: tuple[torch.Tensor, ...],
-        reference: torch.Tensor,
-        device: torch.device,
-    ) -> dict[str, TimingResult]:
-        """Time every comparison implementation under the candidates' settings,
-        after checking it against the reference."""
-        out: dict[str, TimingResult] = {}
+    def _baselines(self, operator: Operator, problem: Problem, inputs: tuple[torch.Tensor, ...],
+                   reference: torch.Tensor, device: torch.device) -> dict[str, TimingResult]:
+        """Each comparison implementation, gated like a candidate, then timed
+        with the candidates' warmup, iterations and flush."""
+        timed: dict[str, TimingResult] = {}
         for label, fn in operator.baselines(problem, inputs).items():
             try:
                 check = verify(reference, fn(), dtype=problem.dtype)
-                if not check.passed:
+                if check.passed:
+                    timed[label] = self._time(fn, device)
+                else:
                     self.log(f"  baseline {label} disagrees with the reference: {check.reason}")
-                    continue
-                out[label] = benchmark(
-                    fn,
-                    warmup=self.warmup,
-                    iterations=self.iterations,
-                    device=device,
-                    flush_l2=self.flush_l2,
-                )
             except Exception as exc:
-                _, message = _classify(exc)
-                self.log(f"  baseline {label} unavailable: {message}")
-        return out
+                self.log(f"  baseline {label} unavailable: {_classify(exc)[1]}")
+        return timed
 
-    def _persist(self, result: TuningResult, env: Environment) -> None:
+    # --- persistence ------------------------------------------------------------------
+    def _store_winner(self, result: TuningResult) -> None:
         best = result.best
-        if self.cache is not None and best is not None:
-            self.cache.put(
-                result.problem,
-                env.device_key,
-                best.config,
-                median_us=best.timing.median_us if best.timing else None,
-                timestamp=env.timestamp,
-                candidates_tested=result.tested,
-            )
+        if self.cache is None or best is None:
+            return
+        self.cache.put(result.problem, result.environment.device_key, best.config,
+                       median_us=best.timing.median_us if best.timing else None,
+                       timestamp=result.environment.timestamp,
+                       candidates_tested=result.tested)
+
+    def _record(self, result: TuningResult) -> None:
         if self.db is None:
             return
         from kernelforge import __version__
 
-        run_id = self.db.start_run(env, notes="tune", version=__version__)
-        rows = []
-        for o in result.outcomes:
-            ms = o.timing.median_ms if o.timing else None
-            rows.append(
-                Measurement(
-                    label="kernelforge",
-                    status=o.status,
-                    config=o.config,
-                    verification=o.verification,
-                    timing=o.timing,
-                    tflops=result.tflops(ms) if ms else None,
-                    gbps=result.gbps(ms) if ms else None,
-                    error=o.error,
-                )
-            )
-        for label, timing in result.baselines.items():
-            rows.append(
-                Measurement(
-                    label=label,
-                    status=STATUS_OK,
-                    timing=timing,
-                    tflops=result.tflops(timing.median_ms),
-                    gbps=result.gbps(timing.median_ms),
-                )
-            )
+        def rates(timing: TimingResult | None) -> dict[str, float | None]:
+            if timing is None:
+                return {"tflops": None, "gbps": None}
+            return {"tflops": result.tflops(timing.median_ms), "gbps": result.gbps(timing.median_ms)}
+
+        rows = [Measurement(label=TUNED_LABEL, status=o.status, config=o.config,
+                            verification=o.verification, timing=o.timing, error=o.error,
+                            **rates(o.timing))
+                for o in result.outcomes]
+        rows += [Measurement(label=label, status=STATUS_OK, timing=t, **rates(t))
+                 for label, t in result.baselines.items()]
+        run_id = self.db.start_run(result.environment, notes="tune", version=__version__)
         self.db.record_many(run_id, result.problem, rows)
