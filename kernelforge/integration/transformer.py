@@ -1,22 +1,24 @@
-"""A pre-norm decoder block whose norms and MLP activation run on kernelforge.
+"""A pre-norm decoder block whose norms and MLP up-projection run on kernelforge.
 
-The dispatch consumer of the reference (kernelforge/integration/
-transformer.py:71-187): the first caller that takes its kernel configurations
-from the winner cache rather than from a tuning run. What it shows is
-Amdahl's law at block scale: the two RMSNorms and the MLP up-projection with
-its bias + GELU are swapped for this package's kernels, while attention
-(``scaled_dot_product_attention``) and the QKV, output and down projections
-stay on PyTorch, so the block-level speedup is bounded by the share of block
-time the swapped operators held.
+The first consumer of the winner cache (kernelforge/integration/
+transformer.py:71-187 plays the same role): it never tunes, it asks dispatch
+for each kernel's configuration and runs it. It shows Amdahl's law at block
+scale. Two operator paths implement the swappable pieces:
 
-``backend`` is a mutable attribute of one module, so both backends run on the
-same weights and a difference in output can only come from the kernels.
+* ``torch``: RMSNorm as the reference formula, the MLP up-projection as
+  ``nn.Linear`` followed by tanh-GELU (three launches);
+* ``kernelforge``: the RMSNorm row kernel, and the up-projection with bias +
+  GELU fused into one MFMA GEMM launch (the split-K GEMV at decode rows).
 
-On MI355X the swapped MLP up-projection takes the direct-to-LDS MFMA GEMM
-with the fused epilogue for prefill rows and the split-K GEMV (same
-epilogue) for decode rows (M <= 8), whichever the cached or packaged winner
-names; ``mlp_up.weight.t()`` is consumed through its strides (B k-contiguous),
-so no transposed copy is made.
+Attention (``scaled_dot_product_attention``) and the QKV, output and down
+projections are PyTorch on both paths, so the block-level speedup is bounded
+by the share of block time the swapped operators hold. ``backend`` is a
+mutable attribute of one module: both paths run on the same weights, so a
+difference in output can only come from the kernels.
+
+The parameter names (``attn_norm_weight``, ``mlp_norm_weight``, ``qkv_proj``,
+``out_proj``, ``mlp_up``, ``mlp_down``) and the QKV row order (q, then k,
+then v) are the reference's, so state dicts load into either.
 """
 
 from __future__ import annotations
@@ -40,9 +42,9 @@ BACKENDS = (BACKEND_TORCH, BACKEND_KERNELO)
 
 @dataclass(frozen=True)
 class BlockConfig:
-    """Geometry of one block; the default is Llama-2-7B's (4096 hidden, 32
-    heads, 11008 intermediate). The MLP is GELU rather than SwiGLU because the
-    fused kernel's epilogue is bias + GELU; the matrix shapes are the real ones."""
+    """Block geometry. Defaults are Llama-2-7B's matrix shapes (hidden 4096, 32
+    heads, MLP 11008); the MLP is GELU rather than SwiGLU because the fused
+    epilogue is bias + tanh-GELU."""
 
     hidden: int = 4096
     heads: int = 32
@@ -50,7 +52,7 @@ class BlockConfig:
     eps: float = DEFAULT_EPS
 
     def __post_init__(self) -> None:
-        if self.hidden % self.heads:
+        if self.hidden % self.heads != 0:
             raise ValueError(f"hidden {self.hidden} is not divisible by {self.heads} heads")
 
     @property
@@ -58,8 +60,53 @@ class BlockConfig:
         return self.hidden // self.heads
 
 
+class _TorchPath:
+    """The swappable operators in plain PyTorch."""
+
+    def norm(self, block: TransformerBlock, rows: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+        return rmsnorm_reference(rows, weight, eps=block.config.eps)
+
+    def up_gelu(self, block: TransformerBlock, rows: torch.Tensor) -> torch.Tensor:
+        return F.gelu(block.mlp_up(rows), approximate="tanh")
+
+
+class _KernelPath:
+    """The swappable operators on this package's kernels, configured by dispatch.
+
+    A configuration is looked up once per (operation, rows, dtype) and kept:
+    dispatch reads cache files, and a block runs many forwards per shape.
+    """
+
+    def __init__(self, cache: ConfigCache | None) -> None:
+        self.cache = cache
+        self.chosen: dict[tuple[str, int, torch.dtype], KernelConfig] = {}
+
+    def _config(self, block: TransformerBlock, operation: str, rows: int,
+                dtype: torch.dtype) -> KernelConfig:
+        key = (operation, rows, dtype)
+        if key not in self.chosen:
+            from kernelforge.kernels import get_operator
+
+            geo = block.config
+            dims = ({"rows": rows, "cols": geo.hidden} if operation == "rmsnorm"
+                    else {"M": rows, "N": geo.intermediate, "K": geo.hidden})
+            problem = Problem.create(operation, dtype, **dims)
+            self.chosen[key] = select_config(get_operator(operation), problem, cache=self.cache).config
+        return self.chosen[key]
+
+    def norm(self, block: TransformerBlock, rows: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+        cfg = self._config(block, "rmsnorm", rows.shape[0], rows.dtype)
+        return rmsnorm(rows, weight, eps=block.config.eps, config=cfg)
+
+    def up_gelu(self, block: TransformerBlock, rows: torch.Tensor) -> torch.Tensor:
+        cfg = self._config(block, "fused_linear", rows.shape[0], rows.dtype)
+        # nn.Linear keeps its weight as (out, in); the transposed view is the
+        # (K, N) operand with k-contiguous columns, read through its strides.
+        return fused_linear_gelu(rows, block.mlp_up.weight.t(), block.mlp_up.bias, config=cfg)
+
+
 class TransformerBlock(nn.Module):
-    """Pre-norm decoder block with swappable normalisation and MLP activation."""
+    """Pre-norm decoder block: x + attn(norm(x)), then x + mlp(norm(x))."""
 
     def __init__(
         self,
@@ -71,66 +118,47 @@ class TransformerBlock(nn.Module):
         cache: ConfigCache | None = None,
     ) -> None:
         super().__init__()
-        if backend not in BACKENDS:
-            raise ValueError(f"backend must be one of {BACKENDS}, got {backend!r}")
         self.config = config or BlockConfig()
+        self._paths = {BACKEND_TORCH: _TorchPath(), BACKEND_KERNELO: _KernelPath(cache)}
         self.backend = backend
-        self._cache = cache
-        # Selection reads the cache files; it runs once per (operation, shape).
-        self._selected: dict[tuple[str, int, int], KernelConfig] = {}
+        h, inter = self.config.hidden, self.config.intermediate
+        opts = {"device": device, "dtype": dtype}
+        self.attn_norm_weight = nn.Parameter(torch.ones(h, **opts))
+        self.mlp_norm_weight = nn.Parameter(torch.ones(h, **opts))
+        self.qkv_proj = nn.Linear(h, 3 * h, bias=False, **opts)
+        self.out_proj = nn.Linear(h, h, bias=False, **opts)
+        self.mlp_up = nn.Linear(h, inter, bias=True, **opts)
+        self.mlp_down = nn.Linear(inter, h, bias=False, **opts)
 
-        hidden, intermediate = self.config.hidden, self.config.intermediate
-        factory = {"device": device, "dtype": dtype}
-        self.attn_norm_weight = nn.Parameter(torch.ones(hidden, **factory))
-        self.mlp_norm_weight = nn.Parameter(torch.ones(hidden, **factory))
-        self.qkv_proj = nn.Linear(hidden, 3 * hidden, bias=False, **factory)
-        self.out_proj = nn.Linear(hidden, hidden, bias=False, **factory)
-        self.mlp_up = nn.Linear(hidden, intermediate, bias=True, **factory)
-        self.mlp_down = nn.Linear(intermediate, hidden, bias=False, **factory)
+    @property
+    def backend(self) -> str:
+        return self._backend
 
-    def _config_for(self, operation: str, rows: int, cols: int, dtype: torch.dtype) -> KernelConfig:
-        key = (operation, rows, cols)
-        cfg = self._selected.get(key)
-        if cfg is None:
-            from kernelforge.kernels import get_operator
+    @backend.setter
+    def backend(self, value: str) -> None:
+        if value not in BACKENDS:
+            raise ValueError(f"backend must be one of {BACKENDS}, got {value!r}")
+        self._backend = value
 
-            if operation == "rmsnorm":
-                problem = Problem.create(operation, dtype, rows=rows, cols=cols)
-            else:
-                problem = Problem.create(operation, dtype, M=rows, N=self.config.intermediate, K=cols)
-            cfg = select_config(get_operator(operation), problem, cache=self._cache).config
-            self._selected[key] = cfg
-        return cfg
-
-    def _norm(self, flat: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
-        if self.backend == BACKEND_TORCH:
-            return rmsnorm_reference(flat, weight, eps=self.config.eps)
-        cfg = self._config_for("rmsnorm", flat.shape[0], flat.shape[1], flat.dtype)
-        return rmsnorm(flat, weight, eps=self.config.eps, config=cfg)
-
-    def _mlp_activation(self, flat: torch.Tensor) -> torch.Tensor:
-        if self.backend == BACKEND_TORCH:
-            return F.gelu(self.mlp_up(flat), approximate="tanh")
-        cfg = self._config_for("fused_linear", flat.shape[0], flat.shape[1], flat.dtype)
-        return fused_linear_gelu(flat, self.mlp_up.weight.t(), self.mlp_up.bias, config=cfg)
+    def _attention(self, rows: torch.Tensor, batch: int, seq: int) -> torch.Tensor:
+        geo = self.config
+        # (tokens, 3*hidden) -> three (batch, heads, seq, head_dim) views.
+        q, k, v = (self.qkv_proj(rows).view(batch, seq, 3, geo.heads, geo.head_dim)
+                   .permute(2, 0, 3, 1, 4).unbind(0))
+        mixed = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+        return self.out_proj(mixed.transpose(1, 2).reshape(batch * seq, geo.hidden))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if x.ndim != 3:
+        if x.dim() != 3:
             raise ValueError(f"expected (batch, seq, hidden), got {tuple(x.shape)}")
-        batch, seq, hidden = x.shape
-        if hidden != self.config.hidden:
-            raise ValueError(f"expected hidden {self.config.hidden}, got {hidden}")
-        heads, head_dim = self.config.heads, self.config.head_dim
-        tokens = batch * seq
-
-        normed = self._norm(x.reshape(tokens, hidden), self.attn_norm_weight)
-        qkv = self.qkv_proj(normed).view(batch, seq, 3, heads, head_dim)
-        q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
-        attended = F.scaled_dot_product_attention(q, k, v, is_causal=True)
-        x = x + self.out_proj(attended.transpose(1, 2).reshape(batch, seq, hidden))
-
-        normed = self._norm(x.reshape(tokens, hidden), self.mlp_norm_weight)
-        return x + self.mlp_down(self._mlp_activation(normed)).view(batch, seq, hidden)
+        batch, seq, width = x.shape
+        if width != self.config.hidden:
+            raise ValueError(f"expected hidden {self.config.hidden}, got {width}")
+        path = self._paths[self._backend]
+        rows = x.reshape(batch * seq, width)
+        rows = rows + self._attention(path.norm(self, rows, self.attn_norm_weight), batch, seq)
+        mlp = self.mlp_down(path.up_gelu(self, path.norm(self, rows, self.mlp_norm_weight)))
+        return (rows + mlp).view(batch, seq, width)
 
 
 def benchmark_block(
@@ -144,23 +172,21 @@ def benchmark_block(
     iterations: int = 100,
     cache: ConfigCache | None = None,
 ) -> dict[str, object]:
-    """Time one block per backend on identical weights and inputs.
+    """The latency distribution of one block forward per backend, same weights and input.
 
-    No cache flush between iterations (transformer.py:176-186 in the
-    reference): a block's working set (about 300 MiB of fp16 weights at the
-    default geometry) is larger than L2 plus the Infinity Cache anyway.
+    Unflushed: at the default geometry the block reads about 300 MiB of fp16
+    weights per forward, more than L2 and the Infinity Cache hold, so every
+    iteration already starts cold.
     """
     from kernelforge.benchmark.runner import benchmark
 
     block = TransformerBlock(config, dtype=dtype, device=device, cache=cache)
-    gen = torch.Generator().manual_seed(0)
-    x = torch.randn(batch, seq, block.config.hidden, generator=gen).to(device=device, dtype=dtype)
-    results: dict[str, object] = {}
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(batch, seq, block.config.hidden, generator=g).to(device=device, dtype=dtype)
+    timings: dict[str, object] = {}
     with torch.inference_mode():
-        for backend in BACKENDS:
-            block.backend = backend
-            results[backend] = benchmark(
-                lambda: block(x), warmup=warmup, iterations=iterations, device=device,
-                flush_l2=False,
-            )
-    return results
+        for name in BACKENDS:
+            block.backend = name
+            timings[name] = benchmark(lambda: block(x), warmup=warmup, iterations=iterations,
+                                      device=device, flush_l2=False)
+    return timings

@@ -1,31 +1,28 @@
-"""Kernel attribution with ``torch.profiler`` (launches per call, device time per kernel).
+"""What ran: device kernels per call and their device time, from ``torch.profiler``.
 
-The latency harness says how long; this says *what ran*. For the fusion
-comparison the launch count is the evidence: the unfused sequence launches
-at least three kernels per call, the fused one exactly one
-(kernelforge/profiling/pytorch_profiler.py:53-60,91-135). On ROCm the
-profiler's device activity comes from the HIP runtime, so launches made
-through ``libkernelforge_hip.so`` are attributed like torch's own.
+The event harness says how long a call takes; this says which kernels the
+call launched, which is the evidence for fusion (the unfused linear + bias +
+GELU launches at least three kernels per call, the fused one exactly one;
+kernelforge/profiling/pytorch_profiler.py:53-135 records the same). On ROCm
+the profiler's device activity comes from the HIP runtime's own tracing, so
+launches made through ``libkernelforge_hip.so`` are attributed the same way
+as torch's.
 
-Tracing perturbs timing: these figures are for attribution, not headline
-latency (that comes from the hipEvent harness).
+The raw device events are grouped here by kernel name, not through the
+profiler's own averaging tables, so a record is exactly (name, number of
+device executions, summed device microseconds). Tracing perturbs timing: use
+these figures for attribution, the event harness for latency.
 """
 
 from __future__ import annotations
 
+from collections import defaultdict
+from collections.abc import Callable, Iterable
 from dataclasses import dataclass
 from pathlib import Path
 
 import torch
 from torch.autograd import DeviceType
-
-
-def _device_time_us(event) -> float:
-    for attribute in ("device_time_total", "cuda_time_total"):
-        value = getattr(event, attribute, None)
-        if value is not None:
-            return float(value)
-    return 0.0
 
 
 @dataclass(frozen=True)
@@ -42,79 +39,91 @@ class ProfileResult:
     kernels: tuple[KernelRecord, ...]
     trace_path: Path | None = None
 
+    def _per_call(self, total: float) -> float:
+        return total / self.iterations if self.iterations else 0.0
+
     @property
     def launches_per_iteration(self) -> float:
-        total = sum(k.launches for k in self.kernels)
-        return total / self.iterations if self.iterations else 0.0
+        return self._per_call(sum(k.launches for k in self.kernels))
 
     @property
     def device_time_per_iteration_us(self) -> float:
-        total = sum(k.device_time_us for k in self.kernels)
-        return total / self.iterations if self.iterations else 0.0
+        return self._per_call(sum(k.device_time_us for k in self.kernels))
 
     def render(self, limit: int = 10) -> str:
-        lines = [
-            self.label,
-            f"  kernel launches per call : {self.launches_per_iteration:.2f}",
-            f"  device time per call     : {self.device_time_per_iteration_us:.1f} us",
-        ]
-        if self.kernels:
-            total = max(sum(k.device_time_us for k in self.kernels), 1e-9)
-            width = min(62, max(len(k.name) for k in self.kernels))
-            lines.append("  kernels by device time:")
-            for k in self.kernels[:limit]:
-                lines.append(
-                    f"    {k.name[:width]:<{width}}  "
-                    f"{k.launches / max(self.iterations, 1):>5.1f} launches  "
-                    f"{k.device_time_us / max(self.iterations, 1):>9.1f} us  "
-                    f"{k.device_time_us / total * 100:>5.1f}%"
-                )
+        out = [self.label,
+               f"  kernel launches per call : {self.launches_per_iteration:.2f}",
+               f"  device time per call     : {self.device_time_per_iteration_us:.1f} us"]
+        shown = self.kernels[:limit]
+        if shown:
+            total = sum(k.device_time_us for k in self.kernels) or 1e-9
+            name_w = min(62, max(len(k.name) for k in shown))
+            out.append("  kernels by device time:")
+            for k in shown:
+                out.append(f"    {k.name[:name_w].ljust(name_w)}  "
+                           f"{self._per_call(k.launches):>5.1f} launches  "
+                           f"{self._per_call(k.device_time_us):>9.1f} us  "
+                           f"{100.0 * k.device_time_us / total:>5.1f}%")
         if self.trace_path is not None:
-            lines.append(f"  chrome trace: {self.trace_path}")
-        return "\n".join(lines)
+            out.append(f"  chrome trace: {self.trace_path}")
+        return "\n".join(out)
+
+
+def _device_us(event) -> float:
+    """Duration of one device-side event (a kernel execution), in microseconds."""
+    return float(event.time_range.elapsed_us())
+
+
+def _group(events: Iterable) -> tuple[KernelRecord, ...]:
+    launches: dict[str, int] = defaultdict(int)
+    busy: dict[str, float] = defaultdict(float)
+    for ev in events:
+        if ev.device_type != DeviceType.CUDA:
+            continue
+        us = _device_us(ev)
+        if us <= 0:
+            continue
+        launches[ev.name] += 1
+        busy[ev.name] += us
+    records = (KernelRecord(n, launches[n], busy[n]) for n in launches)
+    return tuple(sorted(records, key=lambda r: (-r.device_time_us, r.name)))
 
 
 def profile_kernels(
-    fn,
+    fn: Callable[[], object],
     *,
     label: str,
     warmup: int = 10,
     iterations: int = 20,
     trace_path: str | Path | None = None,
 ) -> ProfileResult:
-    """Profile ``fn`` and attribute device time to individual kernels."""
+    """Run ``fn`` ``iterations`` times under the profiler and group its device kernels."""
     if not torch.cuda.is_available():
         raise RuntimeError("kernel attribution needs a ROCm device")
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    activities = [torch.profiler.ProfilerActivity.CPU, torch.profiler.ProfilerActivity.CUDA]
-    with torch.profiler.profile(activities=activities) as prof:
+    wanted = [torch.profiler.ProfilerActivity.CPU, torch.profiler.ProfilerActivity.CUDA]
+    with torch.profiler.profile(activities=wanted) as prof:
         for _ in range(iterations):
             fn()
         torch.cuda.synchronize()
-    kernels = [
-        KernelRecord(name=e.key, launches=int(e.count), device_time_us=_device_time_us(e))
-        for e in prof.key_averages()
-        if e.device_type == DeviceType.CUDA and _device_time_us(e) > 0
-    ]
-    kernels.sort(key=lambda k: -k.device_time_us)
-    resolved = None
+    saved = None
     if trace_path is not None:
-        resolved = Path(trace_path)
-        resolved.parent.mkdir(parents=True, exist_ok=True)
-        prof.export_chrome_trace(str(resolved))
-    return ProfileResult(label=label, iterations=iterations, kernels=tuple(kernels), trace_path=resolved)
+        saved = Path(trace_path)
+        saved.parent.mkdir(parents=True, exist_ok=True)
+        prof.export_chrome_trace(str(saved))
+    return ProfileResult(label, iterations, _group(prof.events()), saved)
 
 
-def launches_per_iteration(fn, *, warmup: int = 3, iterations: int = 5) -> float:
+def launches_per_iteration(fn: Callable[[], object], *, warmup: int = 3,
+                           iterations: int = 5) -> float:
+    """Device kernels one call of ``fn`` launches, on average."""
     return profile_kernels(fn, label="", warmup=warmup, iterations=iterations).launches_per_iteration
 
 
-def compare_launch_counts(
-    candidates: dict[str, object], *, warmup: int = 10, iterations: int = 20
-) -> list[ProfileResult]:
-    return [
-        profile_kernels(fn, label=label, warmup=warmup, iterations=iterations)
-        for label, fn in candidates.items()
-    ]
+def compare_launch_counts(candidates: dict[str, Callable[[], object]], *, warmup: int = 10,
+                          iterations: int = 20) -> list[ProfileResult]:
+    """:func:`profile_kernels` for each labelled implementation, in order."""
+    return [profile_kernels(fn, label=label, warmup=warmup, iterations=iterations)
+            for label, fn in candidates.items()]

@@ -25,9 +25,10 @@ is unit-testable on a CPU-only host.
 from __future__ import annotations
 
 import math
-
 from abc import ABC, abstractmethod
+from collections import Counter
 from collections.abc import Iterator
+from dataclasses import dataclass
 from itertools import product
 
 from kernelforge.dtypes import itemsize
@@ -79,8 +80,51 @@ def ceil_div(a: int, b: int) -> int:
     return -(-a // b)
 
 
+@dataclass(frozen=True)
+class CandidateSet:
+    """What generation produced for one problem: the candidates in rank order,
+    every rejected grid point with its rule, and the count after each stage."""
+
+    problem: Problem
+    generated: int
+    feasible: int
+    after_prune: int
+    budget: int
+    candidates: list[KernelConfig]
+    rejected: tuple[tuple[KernelConfig, str], ...]
+
+    def __len__(self) -> int:
+        return len(self.candidates)
+
+    def __iter__(self) -> Iterator[KernelConfig]:
+        return iter(self.candidates)
+
+    def rule_counts(self) -> list[tuple[str, int]]:
+        """Rejections per rule name (the text before the first ``:`` or ``(``),
+        most frequent first."""
+        names = Counter(reason.split(":")[0].split("(")[0].strip() for _, reason in self.rejected)
+        return sorted(names.items(), key=lambda kv: (-kv[1], kv[0]))
+
+
+def _fill_prune(programs: dict[KernelConfig, int], cu_count: int) -> set[KernelConfig]:
+    """Configs to drop because their launch fills under half the CUs.
+
+    Applies only when some feasible config fills every CU: for a problem too
+    small to fill the GPU at all, the small launches are the whole answer.
+    """
+    if not programs or max(programs.values()) < cu_count:
+        return set()
+    return {c for c, n in programs.items() if n < cu_count // 2}
+
+
 class SearchSpace(ABC):
-    """The set of configurations worth trying for one operation."""
+    """The configurations worth trying for one operation.
+
+    Subclasses supply the grid, the named rejection rules, the launch size
+    (for the fill prune) and the ranking key; :meth:`generate` runs the
+    stages in a fixed order -- enumerate, reject, prune, rank, budget -- and
+    keeps every count, which is what the published candidate counts pin.
+    """
 
     operation: str
 
@@ -91,160 +135,71 @@ class SearchSpace(ABC):
 
     @abstractmethod
     def grid(self, problem: Problem) -> Iterator[KernelConfig]:
-        """Every point in the unfiltered parameter grid."""
+        """Every point of the unfiltered parameter grid."""
 
     @abstractmethod
     def reject_reason(self, config: KernelConfig, problem: Problem, caps: DeviceCaps) -> str | None:
-        """Why ``config`` is not worth trying, or ``None`` to keep it."""
+        """The named rule that rules ``config`` out, or ``None`` to keep it."""
 
     def num_programs(self, config: KernelConfig, problem: Problem) -> int:
-        """Workgroups in the launch grid, used by the utilisation prune."""
+        """Workgroups the launch makes; spaces without a model skip the fill prune."""
         raise NotImplementedError
 
-    def priority(
-        self, config: KernelConfig, problem: Problem, caps: DeviceCaps
-    ) -> tuple[float, ...]:
-        """Sort key for the budget; lower sorts first. Ties break on the JSON form."""
+    def priority(self, config: KernelConfig, problem: Problem, caps: DeviceCaps) -> tuple[float, ...]:
+        """Ranking key, lower first; ties break on the canonical JSON."""
         return (0.0,)
 
-    def candidates(
-        self,
-        problem: Problem,
-        caps: DeviceCaps | None = None,
-        *,
-        max_candidates: int | None = None,
-    ) -> list[KernelConfig]:
+    def candidates(self, problem: Problem, caps: DeviceCaps | None = None, *,
+                   max_candidates: int | None = None) -> list[KernelConfig]:
         return self.generate(problem, caps, max_candidates=max_candidates).candidates
 
-    def generate(
-        self,
-        problem: Problem,
-        caps: DeviceCaps | None = None,
-        *,
-        max_candidates: int | None = None,
-    ) -> CandidateSet:
+    def generate(self, problem: Problem, caps: DeviceCaps | None = None, *,
+                 max_candidates: int | None = None) -> CandidateSet:
         if problem.operation != self.operation:
             raise ValueError(
-                f"{type(self).__name__} handles {self.operation!r}, got {problem.operation!r}"
-            )
-        caps = caps if caps is not None else device_caps()
-        budget = max_candidates if max_candidates is not None else self.max_candidates
+                f"{type(self).__name__} handles {self.operation!r}, got {problem.operation!r}")
+        machine = caps or device_caps()
+        budget = self.max_candidates if max_candidates is None else max_candidates
         if budget < 1:
             raise ValueError(f"max_candidates must be positive, got {budget}")
 
-        rejected: list[tuple[KernelConfig, str]] = []
-        kept: list[KernelConfig] = []
-        generated = 0
-        for config in self.grid(problem):
-            generated += 1
-            reason = self.reject_reason(config, problem, caps)
-            if reason is None:
-                kept.append(config)
-            else:
-                rejected.append((config, reason))
+        points = list(self.grid(problem))
+        verdicts = [(c, self.reject_reason(c, problem, machine)) for c in points]
+        rejected = [(c, why) for c, why in verdicts if why is not None]
+        feasible = [c for c, why in verdicts if why is None]
 
-        feasible = len(kept)
-        kept, pruned = self._prune_underutilised(kept, problem, caps)
-        rejected.extend(pruned)
-        kept.sort(key=lambda c: (*self.priority(c, problem, caps), c.to_json()))
-        return CandidateSet(
-            problem=problem,
-            generated=generated,
-            feasible=feasible,
-            after_prune=len(kept),
-            budget=budget,
-            candidates=kept[:budget],
-            rejected=tuple(rejected),
-        )
-
-    def _prune_underutilised(
-        self, configs: list[KernelConfig], problem: Problem, caps: DeviceCaps
-    ) -> tuple[list[KernelConfig], list[tuple[KernelConfig, str]]]:
-        """Drop launches that fill under half the CUs, unless none fills them all."""
         try:
-            programs = {c: self.num_programs(c, problem) for c in configs}
+            programs = {c: self.num_programs(c, problem) for c in feasible}
         except NotImplementedError:
-            return configs, []
-        if not programs or max(programs.values()) < caps.cu_count:
-            return configs, []
-        floor = caps.cu_count // 2
-        kept = [c for c in configs if programs[c] >= floor]
-        dropped = [
-            (
-                c,
-                f"underfilled: launch grid of {programs[c]} workgroups fills under half of "
-                f"{caps.cu_count} CUs",
-            )
-            for c in configs
-            if programs[c] < floor
-        ]
-        return kept, dropped
+            programs = {}
+        dropped = _fill_prune(programs, machine.cu_count)
+        rejected += [(c, f"underfilled: launch grid of {programs[c]} workgroups fills under half "
+                         f"of {machine.cu_count} CUs") for c in feasible if c in dropped]
+        survivors = [c for c in feasible if c not in dropped]
+        ranked = sorted(survivors, key=lambda c: (*self.priority(c, problem, machine), c.to_json()))
+        return CandidateSet(problem=problem, generated=len(points), feasible=len(feasible),
+                            after_prune=len(ranked), budget=budget, candidates=ranked[:budget],
+                            rejected=tuple(rejected))
 
     def explain(self, problem: Problem, caps: DeviceCaps | None = None) -> str:
-        """Human-readable breakdown of the filtering, for ``tune --explain``."""
-        resolved = caps if caps is not None else device_caps()
-        result = self.generate(problem, resolved)
-        suffix = "" if resolved.measured else "  <- no device attached"
+        """The stage counts and rejections by rule, for ``tune --explain``."""
+        machine = caps or device_caps()
+        out = self.generate(problem, machine)
+        note = "" if machine.measured else "  <- no device attached"
         lines = [
-            f"{problem.describe()}",
-            f"  device           : {resolved.name} ({resolved.arch}), {resolved.cu_count} CUs, "
-            f"{resolved.lds_per_workgroup // 1024} KiB LDS/workgroup, "
-            f"wave{resolved.wave_size}{suffix}",
-            f"  grid points      : {result.generated}",
-            f"  feasible         : {result.feasible}",
-            f"  after prune      : {result.after_prune}",
-            f"  selected (budget): {len(result.candidates)} of {result.budget}",
+            problem.describe(),
+            f"  device           : {machine.name} ({machine.arch}), {machine.cu_count} CUs, "
+            f"{machine.lds_per_workgroup // 1024} KiB LDS/workgroup, wave{machine.wave_size}{note}",
+            f"  grid points      : {out.generated}",
+            f"  feasible         : {out.feasible}",
+            f"  after prune      : {out.after_prune}",
+            f"  selected (budget): {len(out.candidates)} of {out.budget}",
         ]
-        reasons: dict[str, int] = {}
-        for _, reason in result.rejected:
-            key = reason.split(":")[0].split("(")[0].strip()
-            reasons[key] = reasons.get(key, 0) + 1
-        if reasons:
+        counts = out.rule_counts()
+        if counts:
             lines.append("  rejections by rule:")
-            lines.extend(
-                f"    {count:>4}  {reason}"
-                for reason, count in sorted(reasons.items(), key=lambda kv: (-kv[1], kv[0]))
-            )
+            lines += [f"    {n:>4}  {rule}" for rule, n in counts]
         return "\n".join(lines)
-
-
-class CandidateSet:
-    """Candidates plus the counts at each stage of generation."""
-
-    __slots__ = (
-        "problem",
-        "generated",
-        "feasible",
-        "after_prune",
-        "budget",
-        "candidates",
-        "rejected",
-    )
-
-    def __init__(
-        self,
-        *,
-        problem: Problem,
-        generated: int,
-        feasible: int,
-        after_prune: int,
-        budget: int,
-        candidates: list[KernelConfig],
-        rejected: tuple[tuple[KernelConfig, str], ...],
-    ) -> None:
-        self.problem = problem
-        self.generated = generated
-        self.feasible = feasible
-        self.after_prune = after_prune
-        self.budget = budget
-        self.candidates = candidates
-        self.rejected = rejected
-
-    def __len__(self) -> int:
-        return len(self.candidates)
-
-    def __iter__(self) -> Iterator[KernelConfig]:
-        return iter(self.candidates)
 
 
 # ---------------------------------------------------------------------------

@@ -18,7 +18,6 @@ from kernelforge.runtime.env import capture_environment
 from kernelforge.testing import VerificationResult
 from kernelforge.tuning.config import KernelConfig, Problem
 
-pytest.importorskip("pandas")
 pytest.importorskip("matplotlib")
 
 
