@@ -234,12 +234,13 @@ __global__ __launch_bounds__(max_lanes<EPT>()) void rmsnorm_rows(const T* __rest
   const int t = threadIdx.x;
   const int nt = blockDim.x;
   const int nwaves = nt / kWave;
-  // gamma is shared by all rows of the program: read it once.
-  RowTile<T, EPT> g;
-  g.load(gamma, cols, t, nt, vec, 0.f);
   const float inv_cols = 1.0f / static_cast<float>(cols);
   using Tile = RowTile<T, EPT>;
-  auto process = [&](Tile& tile, int64_t r) {
+  // gamma is shared by all rows of the program and read once. On the vector
+  // path its loads are issued after the first row's and converted only when
+  // the first row is stored, so the two latencies overlap instead of adding
+  // up at the start of every workgroup.
+  auto process = [&](Tile& tile, int64_t r, const Tile& g) {
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) ss = __builtin_fmaf(tile.v[e], tile.v[e], ss);
@@ -249,29 +250,48 @@ __global__ __launch_bounds__(max_lanes<EPT>()) void rmsnorm_rows(const T* __rest
                [inv_rms, &g](float v, int e) { return (v * inv_rms) * g.v[e]; });
   };
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rpp;
+  if (r0 >= rows) return;
   // Out-of-row lanes hold 0, which adds nothing to the sum of squares.
-  if constexpr (prefetch_rows<T, EPT>()) {
-    if (Tile::vector_ok(vec, cols)) {
-      typename Tile::Raw cur, nxt;
-      if (r0 < rows) Tile::load_raw(cur, x + r0 * xrs, cols, t, nt);
-      for (int i = 0; i < rpp; ++i) {
-        const int64_t r = r0 + i;
-        if (r >= rows) break;
+  if constexpr (Tile::kVector) {
+  if (Tile::vector_ok(vec, cols)) {
+    typename Tile::Raw cur, graw;
+    Tile::load_raw(cur, x + r0 * xrs, cols, t, nt);
+    Tile::load_raw(graw, gamma, cols, t, nt);
+    Tile g;
+    bool have_gamma = false;
+    for (int i = 0; i < rpp; ++i) {
+      const int64_t r = r0 + i;
+      if (r >= rows) break;
+      typename Tile::Raw nxt;
+      // Rows of at most four vectors per lane keep the next row in flight
+      // during this row's reduction.
+      if constexpr (prefetch_rows<T, EPT>()) {
         if (i + 1 < rpp && r + 1 < rows) Tile::load_raw(nxt, x + (r + 1) * xrs, cols, t, nt);
-        Tile tile;
-        tile.convert(cur, cols, t, nt, 0.f);
-        process(tile, r);
-        cur = nxt;
       }
-      return;
+      Tile tile;
+      tile.convert(cur, cols, t, nt, 0.f);
+      if (!have_gamma) {
+        g.convert(graw, cols, t, nt, 0.f);
+        have_gamma = true;
+      }
+      process(tile, r, g);
+      if constexpr (prefetch_rows<T, EPT>()) {
+        cur = nxt;
+      } else if (i + 1 < rpp && r + 1 < rows) {
+        Tile::load_raw(cur, x + (r + 1) * xrs, cols, t, nt);
+      }
     }
+    return;
   }
+  }
+  Tile g;
+  g.load(gamma, cols, t, nt, vec, 0.f);
   for (int i = 0; i < rpp; ++i) {
     const int64_t r = r0 + i;
     if (r >= rows) break;
     Tile tile;
     tile.load(x + r * xrs, cols, t, nt, vec, 0.f);
-    process(tile, r);
+    process(tile, r, g);
   }
 }
 

@@ -66,8 +66,13 @@ SIMDS_PER_CU = 4
 #: MFMA "MOPS" count 512 FLOPs each (one 16x16x32 16-bit MFMA is 16384 FLOPs, 32 MOPS).
 FLOPS_PER_MOP = 512
 
-#: Kernels of this library carry this namespace in their names.
-LIBRARY_KERNEL_PREFIX = "kf::"
+#: Kernels of this library live in namespace ``kf``; the profiler reports
+#: some names demangled (``void kf::...``) and others mangled (``_ZN2kf...``).
+LIBRARY_KERNEL_MARKS = ("kf::", "_ZN2kf")
+
+
+def is_library_kernel(name: str) -> bool:
+    return any(mark in name for mark in LIBRARY_KERNEL_MARKS)
 
 
 def rocprof_available() -> bool:
@@ -170,7 +175,7 @@ def parse_trace_csv(path: str | Path) -> list[Dispatch]:
 def measured_dispatch(dispatches: list[Dispatch]) -> Dispatch | None:
     """The launch-once child's measured launch: its last dispatch of a library kernel
     (the child warms the kernel up once before flushing the caches and measuring)."""
-    ours = [d for d in dispatches if LIBRARY_KERNEL_PREFIX in d.kernel]
+    ours = [d for d in dispatches if is_library_kernel(d.kernel)]
     return ours[-1] if ours else None
 
 

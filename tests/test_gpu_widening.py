@@ -288,9 +288,10 @@ def test_block_resolves_configurations_once_per_shape():
     x = _randn(1, 64, 256, dtype=torch.float16, seed=32).to(DEV)
     with torch.inference_mode():
         block(x)
-        resolved = dict(block._selected)
+        chosen = block._paths["kernelforge"].chosen
+        resolved = dict(chosen)
         block(x)
-    assert block._selected == resolved
+    assert chosen == resolved
     assert {op for op, _, _ in resolved} == {"rmsnorm", "fused_linear"}
 
 

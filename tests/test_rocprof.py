@@ -86,6 +86,9 @@ def test_counter_csv_groups_by_dispatch_and_picks_the_last_library_launch(tmp_pa
     assert launch.mfma_utilisation == pytest.approx(0.538, abs=5e-4)
     assert launch.mfma_flops == 2 * 2048 * 4096 * 4096
     assert rocprof.measured_dispatch([d for d in dispatches if d.kernel == FILL]) is None
+    # The profiler reports the GEMM kernels by their mangled names.
+    mangled = "_ZN2kf4gemm18gemm_direct_kernelIDF16_Li128ELi256ELi8ELi0ELi3EEEvNS0_4ArgsE"
+    assert rocprof.is_library_kernel(mangled) and not rocprof.is_library_kernel(FILL)
 
 
 def test_trace_csv_supplies_duration_and_launch_shape(tmp_path):
