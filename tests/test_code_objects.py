@@ -111,11 +111,15 @@ def test_softmax_is_one_exp_per_element(kernels):
 
 
 def _row_copies(name):
-    """Row loops in the code object: rows of 1-4 vectors per lane carry a second,
-    prefetching copy of the loop (rows.hip prefetch_rows)."""
+    """Row loops in the code object. Softmax rows of 1-4 vectors per lane carry a
+    second, prefetching copy of the loop (rows.hip prefetch_rows); RMSNorm has a
+    separate vector-path loop whenever a lane holds at least one whole vector
+    (it issues gamma's loads behind the first row's)."""
     m = re.search(r"_rowsI(f|DF16_|DF16b)Li(\d+)E", name)
     size = 4 if m.group(1) == "f" else 2
     ept = int(m.group(2))
+    if "rmsnorm_rows" in name:
+        return 2 if ept * size >= 16 else 1
     return 2 if (ept >= 16 // size and ept * size <= 64) else 1
 
 
