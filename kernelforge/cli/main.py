@@ -591,9 +591,14 @@ def _profile_rocprof(session: _Session) -> int:
         out_dir = Path(args.profile_dir) if args.profile_dir else Path(scratch)
         result = rocprof.run(target, out_dir=out_dir, passes=tuple(args.passes))
     print(_problem_banner(problem))
-    print(result.render(flops=operator.flops(problem), algorithmic_bytes=operator.bytes_moved(problem),
-                        peak_tflops=MI355X_CAPS.peak_fp16_tflops, peak_gbps=MI355X_CAPS.peak_hbm_gbps,
-                        cu_count=MI355X_CAPS.cu_count, memory_bound=operator.is_memory_bound()))
+    flops, moved = operator.flops(problem), operator.bytes_moved(problem)
+    # A product below the ridge point (peak FLOP/s over peak bytes/s, about
+    # 315 FLOP/byte for 16-bit MFMA) is bandwidth-bound, e.g. a decode GEMV.
+    ridge = MI355X_CAPS.peak_fp16_tflops * 1e3 / MI355X_CAPS.peak_hbm_gbps
+    bound_by_hbm = operator.is_memory_bound() or flops < ridge * moved
+    print(result.render(flops=flops, algorithmic_bytes=moved, peak_tflops=MI355X_CAPS.peak_fp16_tflops,
+                        peak_gbps=MI355X_CAPS.peak_hbm_gbps, cu_count=MI355X_CAPS.cu_count,
+                        memory_bound=bound_by_hbm))
     return 0 if result.ok else 1
 
 

@@ -134,3 +134,37 @@ def test_row_reductions_use_cross_lane_ops_and_one_barrier_per_reduction(kernels
                                                "v_permlane16_swap_b32")) + sum(
                 1 for line in k.asm if "row_" in line or "quad_perm" in line)
             assert xlane >= 6, name
+
+
+def _operands(line):
+    return line.split("//")[0]
+
+
+def test_split_k_partials_move_with_the_agent_coherent_cache_policy(kernels):
+    """Split-K partial sums cross XCDs, whose L2s are not coherent with each
+    other. The protocol relies on every partial store and load carrying sc1
+    (what the compiler emits for an agent-scope atomic store or load on gfx950),
+    so a compiler that dropped it would show up here rather than as stale sums.
+
+    * GEMV (16-bit, one x row): 32-bit global stores and loads touch only the
+      workspace (y is 16-bit, x and W are read as vectors), so every one must
+      carry sc1; the ticket is an atomic add that returns its value.
+    * Direct GEMM: the partial tiles move through 16-byte buffer stores and
+      loads, the only buffer accesses in the kernel.
+    """
+    seen_gemv = seen_gemm = 0
+    for name, k in kernels.items():
+        if re.search(r"gemv_(splitk|dot)IDF16[_b]Li1E", name):
+            ops = [l for l in k.asm if l.split(None, 1)[0] in ("global_store_dword", "global_load_dword")]
+            assert ops, name
+            assert all("sc1" in _operands(l) for l in ops), (name, [l for l in ops if "sc1" not in l])
+            atomics = [l for l in k.asm if l.split(None, 1)[0].startswith("global_atomic_add")]
+            assert len(atomics) == 1 and "sc0" in _operands(atomics[0]), name
+            seen_gemv += 1
+        params = _gemm_params(name)
+        if params and params[0]:
+            ops = [l for l in k.asm if l.split(None, 1)[0] in ("buffer_store_dwordx4", "buffer_load_dwordx4")]
+            assert ops, name
+            assert all("sc1" in _operands(l) for l in ops), name
+            seen_gemm += 1
+    assert seen_gemv == 2 * 2 * 4 and seen_gemm > 0
