@@ -15,9 +15,9 @@
 //     pass does not track it; every wait for it is explicit. (Untracked
 //     in-order loads can only make the compiler's own waits longer.)
 //   * No padding: LDS rows are dense and 16-byte chunks are XOR-swizzled by
-//     row. The swizzles keep the fragment reads conflict-free for 16 or 32
-//     lanes per LDS cycle and leave the per-lane offsets invariant under the
-//     row steps the code adds as immediates.
+//     row (swz_k, swz_n below). The swizzles keep the fragment reads at the
+//     conflict-free rate of gfx950's LDS and leave the per-lane offsets
+//     invariant under the row steps the code adds as immediates.
 //   * Row-major B stays n-contiguous in LDS and is read with
 //     ds_read_b64_tr_b16: within a 16-lane group, lane i addressing
 //     (row0 + i/4, col0 + 4*(i%4)) receives column col0+i of rows
@@ -138,14 +138,27 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // Swizzled 16-byte chunk of a k-contiguous row (8 chunks per 128-byte row)
-// and of an n-contiguous B row of ROW_CHUNKS chunks. Both depend on row bits
-// below 16 only; rows r and r + 4 of n-contiguous B share the swizzle.
+// and of an n-contiguous B row of ROW_CHUNKS chunks.
+//
+// gfx950's LDS serves a ds_read_b128 in 4.4 clocks and a ds_read_b64 (or
+// ds_read_b64_tr_b16) in 2.5 clocks when no two lanes of one pass share a
+// bank with different addresses; the 8-byte reads pass lanes 0-31, then
+// 32-63, each over 32 eight-byte bank pairs. The swizzles below were chosen
+// against that rule and measured at those rates, eight waves per CU, for the
+// fragment reads of both MFMA shapes this library uses (16x16x32: 16 rows x
+// 4 lane groups; 32x32x16: 32 rows x 2 lane groups), where the earlier forms
+// took 8.0 (A, one of the two shapes) and 4.0 clocks (B, 32x32x16).
+//
+// k-contiguous: chunk ^ ((row >> 1) & 7) -- row bits 1..3, so rows 16 and 32
+// apart (the fragment steps added as immediates) share it.
+// n-contiguous: row bits 0, 1 and 3 only, so rows r and r + 4 (a fragment's
+// second transposing read) and rows 16 apart share it.
 __device__ __forceinline__ int swz_k(int chunk, int row) {
-  return chunk ^ ((row & 7) ^ ((row >> 3) & 1));
+  return chunk ^ ((row >> 1) & 7);
 }
 template <int ROW_CHUNKS>
 __device__ __forceinline__ int swz_n(int chunk, int row) {
-  if constexpr (ROW_CHUNKS >= 16) return chunk ^ (((row & 3) | ((row >> 1) & 4)) << 1);
+  if constexpr (ROW_CHUNKS >= 16) return chunk ^ (((row & 3) << 2) ^ (((row >> 3) & 1) << 1));
   return chunk ^ ((row & 3) << 1);
 }
 
