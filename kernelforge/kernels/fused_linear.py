@@ -20,6 +20,7 @@ import torch
 from kernelforge.benchmark import metrics
 from kernelforge.kernels.base import Operator, cpu_generator
 from kernelforge.kernels.matmul import _heuristic_config, launch_gemm
+from kernelforge.runtime.dispatch import shipped_config
 from kernelforge.tuning.config import KernelConfig, Problem
 from kernelforge.tuning.search import FusedLinearSearchSpace
 
@@ -53,7 +54,8 @@ def fused_linear_gelu(
         raise ValueError(f"dtype mismatch: {x.dtype}, {w.dtype}, {bias.dtype}")
     m, k = x.shape
     n = w.shape[1]
-    cfg = config or _heuristic_config("fused_linear", m, n, k, x.dtype)
+    cfg = (config or shipped_config("fused_linear", x.dtype, x.device, M=m, N=n, K=k)
+           or _heuristic_config("fused_linear", m, n, k, x.dtype))
     y = torch.empty((m, n), device=x.device, dtype=x.dtype)
     return launch_gemm(x, w, bias, y, cfg)
 

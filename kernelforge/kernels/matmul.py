@@ -23,6 +23,7 @@ from kernelforge.kernels.base import Operator, cpu_generator
 from kernelforge.runtime import hip
 from kernelforge.runtime.env import MI355X_CAPS
 from kernelforge.testing import exact_fp32_matmul
+from kernelforge.runtime.dispatch import shipped_config
 from kernelforge.tuning.config import KernelConfig, Problem
 from kernelforge.tuning.search import GEMV_DEFAULT_LANES_PER_ROW, MatmulSearchSpace
 
@@ -46,11 +47,13 @@ def _check_operands(a: torch.Tensor, b: torch.Tensor) -> None:
 def _heuristic_config(operation: str, m: int, n: int, k: int, dtype: torch.dtype) -> KernelConfig:
     """The search space's top-priority candidate for the MI355X model.
 
-    Deterministic and device-free, so it is the same on every host.
+    Deterministic and device-free, so it is the same on every host. An empty
+    dimension is planned as 1: the launch itself returns at once when M or N
+    is zero.
     """
     from kernelforge.tuning.search import search_space
 
-    problem = Problem.create(operation, dtype, M=m, N=n, K=k)
+    problem = Problem.create(operation, dtype, M=max(m, 1), N=max(n, 1), K=max(k, 1))
     best = search_space(operation).candidates(problem, MI355X_CAPS, max_candidates=1)
     return best[0] if best else DEFAULT_CONFIG
 
@@ -136,7 +139,8 @@ def matmul(a: torch.Tensor, b: torch.Tensor, *, config: KernelConfig | None = No
     _check_operands(a, b)
     m, k = a.shape
     n = b.shape[1]
-    cfg = config or _heuristic_config("matmul", m, n, k, a.dtype)
+    cfg = (config or shipped_config("matmul", a.dtype, a.device, M=m, N=n, K=k)
+           or _heuristic_config("matmul", m, n, k, a.dtype))
     c = torch.empty((m, n), device=a.device, dtype=a.dtype)
     return launch_gemm(a, b, None, c, cfg)
 

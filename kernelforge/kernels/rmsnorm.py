@@ -26,6 +26,7 @@ from kernelforge.dtypes import abi_code
 from kernelforge.kernels.base import Operator, cpu_generator
 from kernelforge.kernels.softmax import _check_row_config
 from kernelforge.runtime import hip
+from kernelforge.runtime.dispatch import shipped_config
 from kernelforge.tuning.config import KernelConfig, Problem
 from kernelforge.tuning.search import RMSNormSearchSpace, default_row_config
 
@@ -58,7 +59,8 @@ def rmsnorm(
         raise ValueError("gamma must be contiguous")
     if gamma.dtype != x.dtype:
         raise ValueError(f"dtype mismatch: {x.dtype} vs {gamma.dtype}")
-    cfg = config or default_config(n_cols, x.dtype)
+    cfg = (config or shipped_config("rmsnorm", x.dtype, x.device, rows=n_rows, cols=n_cols)
+           or default_config(n_cols, x.dtype))
     if cfg.get("TWO_PASS"):
         return _rmsnorm_two_pass(x, gamma, float(eps), cfg)
     _check_row_config(cfg, n_cols, RMSNormSearchSpace.MAX_BLOCK_SIZE, "hidden size")

@@ -20,6 +20,7 @@ from kernelforge.benchmark import metrics
 from kernelforge.dtypes import abi_code
 from kernelforge.kernels.base import Operator, cpu_generator
 from kernelforge.runtime import hip
+from kernelforge.runtime.dispatch import shipped_config
 from kernelforge.tuning.config import KernelConfig, Problem
 from kernelforge.tuning.search import SoftmaxSearchSpace, default_row_config
 
@@ -49,7 +50,8 @@ def softmax(x: torch.Tensor, *, config: KernelConfig | None = None) -> torch.Ten
             "copy is not hidden inside a measured region."
         )
     n_rows, n_cols = x.shape
-    cfg = config or default_config(n_cols)
+    cfg = (config or shipped_config("softmax", x.dtype, x.device, rows=n_rows, cols=n_cols)
+           or default_config(n_cols))
     _check_row_config(cfg, n_cols, SoftmaxSearchSpace.MAX_BLOCK_SIZE, "row width")
     out = torch.empty_like(x, memory_format=torch.contiguous_format)
     hip.require_device_tensor(x)

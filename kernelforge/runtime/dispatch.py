@@ -10,6 +10,7 @@ reads in microseconds.
 from __future__ import annotations
 
 from dataclasses import dataclass
+from functools import lru_cache
 
 import torch
 
@@ -73,3 +74,28 @@ def select_config(
         if hit is not None:
             return Selection(config=hit, source=SOURCE_PACKAGED, device_key=key)
     return Selection(config=operator.default_config(problem), source=SOURCE_DEFAULT, device_key=key)
+
+
+@lru_cache(maxsize=4096)
+def _shipped(operation: str, dtype: torch.dtype, dims: tuple, device_index: int) -> KernelConfig | None:
+    shipped = packaged_cache()
+    if shipped is None:
+        return None
+    problem = Problem.create(operation, dtype, **dict(dims))
+    return shipped.get(problem, resolve_device_key(torch.device("cuda", device_index)))
+
+
+def shipped_config(operation: str, dtype: torch.dtype, device: torch.device, **dims: int) -> KernelConfig | None:
+    """The packaged winner for this call's shape on ``device``, if one ships.
+
+    What a kernel entry point runs when the caller passes no configuration
+    (the reference runs its fixed ``DEFAULT_CONFIG`` there, matmul.py:118-120):
+    the winners are fixed per release, so a shape always gets the same
+    configuration, and the lookup is memoised per shape and device so the
+    call costs a dictionary probe. The user's own winner cache is consulted
+    only through ``select_config``, as in the reference.
+    """
+    if device.type != "cuda" or min(dims.values()) < 1:
+        return None
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return _shipped(operation, dtype, tuple(dims.items()), index)

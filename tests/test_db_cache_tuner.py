@@ -283,3 +283,14 @@ def test_hip_error_classes_classify_as_the_tuner_expects():
     assert _classify(hip.KernelOutOfResources("x"))[0] == STATUS_COMPILE_ERROR
     assert _classify(hip.KernelOutOfMemoryError("x"))[0] == STATUS_OOM
     assert _classify(hip.KernelLaunchError("x"))[0] == STATUS_RUNTIME_ERROR
+
+
+def test_shipped_config_is_a_device_lookup_only():
+    """Off the GPU, and for empty shapes, an entry point without a configuration
+    takes the heuristic: there is no shipped winner to look up."""
+    import torch
+
+    from kernelforge.runtime.dispatch import shipped_config
+
+    assert shipped_config("matmul", torch.float16, torch.device("cpu"), M=2048, N=4096, K=4096) is None
+    assert shipped_config("matmul", torch.float16, torch.device("cuda"), M=0, N=4096, K=4096) is None
