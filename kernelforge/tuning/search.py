@@ -515,6 +515,11 @@ class _GemmSpace(SearchSpace):
         if direct:
             wide = bm * bn >= 128 * 128 or (split > 1 and bm * bn >= 64 * 64)
             wave_rank = abs(config["num_warps"] - (8 if wide else 4))
+        elif itemsize(problem.dtype) == 4 and bm * bn >= 256 * 128:
+            # fp32 on the staged pipeline: a 256x128 tile measured 136 TFLOP/s
+            # at 8 waves against 112 at 4 (4096^3); eight waves hide the
+            # fp32 MFMAs' longer issue better than the registers they cost.
+            wave_rank = abs(config["num_warps"] - 8)
         else:
             wave_rank = config["num_warps"]
         return (
