@@ -88,9 +88,11 @@ class _KernelPath:
             from kernelforge.kernels import get_operator
 
             geo = block.config
-            dims = ({"rows": rows, "cols": geo.hidden} if operation == "rmsnorm"
-                    else {"M": rows, "N": geo.intermediate, "K": geo.hidden})
-            problem = Problem.create(operation, dtype, **dims)
+            if operation == "rmsnorm":
+                problem = Problem.create(operation, dtype, rows=rows, cols=geo.hidden)
+            else:  # the MLP weight is read as weight.t(): k-contiguous B
+                problem = Problem.create(operation, dtype, layout="bt", M=rows,
+                                         N=geo.intermediate, K=geo.hidden)
             self.chosen[key] = select_config(get_operator(operation), problem, cache=self.cache).config
         return self.chosen[key]
 

@@ -19,8 +19,7 @@ import torch
 
 from kernelforge.benchmark import metrics
 from kernelforge.kernels.base import Operator, cpu_generator
-from kernelforge.kernels.matmul import _heuristic_config, launch_gemm
-from kernelforge.runtime.dispatch import shipped_config
+from kernelforge.kernels.matmul import _heuristic_config, default_gemm_config, launch_gemm
 from kernelforge.tuning.config import KernelConfig, Problem
 from kernelforge.tuning.search import FusedLinearSearchSpace
 
@@ -52,10 +51,8 @@ def fused_linear_gelu(
         raise ValueError(f"bias must have shape ({w.shape[1]},), got {tuple(bias.shape)}")
     if not (x.dtype == w.dtype == bias.dtype):
         raise ValueError(f"dtype mismatch: {x.dtype}, {w.dtype}, {bias.dtype}")
-    m, k = x.shape
-    n = w.shape[1]
-    cfg = (config or shipped_config("fused_linear", x.dtype, x.device, M=m, N=n, K=k)
-           or _heuristic_config("fused_linear", m, n, k, x.dtype))
+    m, n = x.shape[0], w.shape[1]
+    cfg = config or default_gemm_config("fused_linear", x, w)
     y = torch.empty((m, n), device=x.device, dtype=x.dtype)
     return launch_gemm(x, w, bias, y, cfg)
 
@@ -86,6 +83,8 @@ class FusedLinearOperator(Operator):
         w = torch.randn(d["K"], d["N"], dtype=torch.float32, generator=gen)
         w = (w * (d["K"] ** -0.5)).to(problem.dtype)
         bias = torch.randn(d["N"], dtype=problem.dtype, generator=gen)
+        if problem.layout == "bt":  # an nn.Linear weight passed as weight.t()
+            return x.to(device), w.t().contiguous().to(device).t(), bias.to(device)
         return x.to(device), w.to(device), bias.to(device)
 
     def reference(self, *inputs: torch.Tensor) -> torch.Tensor:
@@ -103,7 +102,7 @@ class FusedLinearOperator(Operator):
 
     def default_config(self, problem: Problem) -> KernelConfig:
         d = problem.dims_dict
-        return _heuristic_config("fused_linear", d["M"], d["N"], d["K"], problem.dtype)
+        return _heuristic_config("fused_linear", d["M"], d["N"], d["K"], problem.dtype, problem.layout)
 
     def flops(self, problem: Problem) -> int:
         d = problem.dims_dict

@@ -43,8 +43,30 @@ def _check_operands(a: torch.Tensor, b: torch.Tensor) -> None:
         raise ValueError(f"dtype mismatch: {a.dtype} vs {b.dtype}")
 
 
+def operand_layout(b: torch.Tensor) -> str:
+    """``"bt"`` when B is read k-contiguous (an ``nn.Linear`` weight passed as
+    ``weight.t()``), else ``""``: the problem layout whose winners apply."""
+    return "bt" if b.stride(0) == 1 and b.shape[0] > 1 and b.stride(1) != 1 else ""
+
+
+def default_gemm_config(operation: str, a: torch.Tensor, b: torch.Tensor) -> KernelConfig:
+    """What an entry point runs without ``config=``: the shipped winner for
+    the shape and B's layout, else the search space's heuristic. A product
+    over k-contiguous B with no winner of its own borrows the row-major
+    winner for MFMA tiles (their pipelines read both layouts at the same
+    speed), but not for the decode GEMV, whose kernel differs by layout."""
+    m, k = a.shape
+    n = b.shape[1]
+    layout = operand_layout(b)
+    cfg = shipped_config(operation, a.dtype, a.device, layout=layout, M=m, N=n, K=k)
+    if cfg is None and layout and m > MatmulSearchSpace.GEMV_MAX_M:
+        cfg = shipped_config(operation, a.dtype, a.device, M=m, N=n, K=k)
+    return cfg or _heuristic_config(operation, m, n, k, a.dtype, layout)
+
+
 @lru_cache(maxsize=1024)
-def _heuristic_config(operation: str, m: int, n: int, k: int, dtype: torch.dtype) -> KernelConfig:
+def _heuristic_config(operation: str, m: int, n: int, k: int, dtype: torch.dtype,
+                      layout: str = "") -> KernelConfig:
     """The search space's top-priority candidate for the MI355X model.
 
     Deterministic and device-free, so it is the same on every host. An empty
@@ -53,7 +75,7 @@ def _heuristic_config(operation: str, m: int, n: int, k: int, dtype: torch.dtype
     """
     from kernelforge.tuning.search import search_space
 
-    problem = Problem.create(operation, dtype, M=max(m, 1), N=max(n, 1), K=max(k, 1))
+    problem = Problem.create(operation, dtype, layout=layout, M=max(m, 1), N=max(n, 1), K=max(k, 1))
     best = search_space(operation).candidates(problem, MI355X_CAPS, max_candidates=1)
     return best[0] if best else DEFAULT_CONFIG
 
@@ -137,10 +159,8 @@ def gemm_availability(cfg: KernelConfig, dtype: torch.dtype) -> str:
 
 def matmul(a: torch.Tensor, b: torch.Tensor, *, config: KernelConfig | None = None) -> torch.Tensor:
     _check_operands(a, b)
-    m, k = a.shape
-    n = b.shape[1]
-    cfg = (config or shipped_config("matmul", a.dtype, a.device, M=m, N=n, K=k)
-           or _heuristic_config("matmul", m, n, k, a.dtype))
+    m, n = a.shape[0], b.shape[1]
+    cfg = config or default_gemm_config("matmul", a, b)
     c = torch.empty((m, n), device=a.device, dtype=a.dtype)
     return launch_gemm(a, b, None, c, cfg)
 
@@ -163,6 +183,8 @@ class MatmulOperator(Operator):
         dims = problem.dims_dict
         a = torch.randn(dims["M"], dims["K"], dtype=problem.dtype, generator=gen)
         b = torch.randn(dims["K"], dims["N"], dtype=problem.dtype, generator=gen)
+        if problem.layout == "bt":  # B read k-contiguous, as from an nn.Linear weight
+            return a.to(device), b.t().contiguous().to(device).t()
         return a.to(device), b.to(device)
 
     def reference(self, *inputs: torch.Tensor) -> torch.Tensor:
@@ -176,7 +198,7 @@ class MatmulOperator(Operator):
 
     def default_config(self, problem: Problem) -> KernelConfig:
         d = problem.dims_dict
-        return _heuristic_config("matmul", d["M"], d["N"], d["K"], problem.dtype)
+        return _heuristic_config("matmul", d["M"], d["N"], d["K"], problem.dtype, problem.layout)
 
     def availability(self, config: KernelConfig, problem: Problem) -> str:
         return gemm_availability(config, problem.dtype)

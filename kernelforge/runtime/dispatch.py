@@ -62,30 +62,46 @@ def select_config(
     use_packaged: bool = True,
 ) -> Selection:
     """Pick the configuration to run ``problem`` with: the user's cache, then
-    the packaged MI355X winners, then the operator default."""
+    the packaged MI355X winners, then the operator default.
+
+    A product over k-contiguous B (``layout="bt"``) looks for winners of its
+    own first; without one, MFMA-tile shapes take the row-major winner (both
+    layouts run the same tile pipelines at the same speed), decode shapes the
+    layout-aware default (their GEMV kernel differs by layout).
+    """
     key = resolve_device_key(device)
     resolved = cache if cache is not None else ConfigCache()
-    cached = resolved.get(problem, key)
-    if cached is not None:
-        return Selection(config=cached, source=SOURCE_CACHE, device_key=key)
     shipped = packaged_cache() if use_packaged else None
-    if shipped is not None:
-        hit = shipped.get(problem, key)
-        if hit is not None:
-            return Selection(config=hit, source=SOURCE_PACKAGED, device_key=key)
+    lookups = [problem]
+    if problem.layout and problem.dims_dict.get("M", 0) > _GEMV_MAX_M:
+        lookups.append(problem.with_layout(""))
+    for candidate in lookups:
+        cached = resolved.get(candidate, key)
+        if cached is not None:
+            return Selection(config=cached, source=SOURCE_CACHE, device_key=key)
+        if shipped is not None:
+            hit = shipped.get(candidate, key)
+            if hit is not None:
+                return Selection(config=hit, source=SOURCE_PACKAGED, device_key=key)
     return Selection(config=operator.default_config(problem), source=SOURCE_DEFAULT, device_key=key)
 
 
+#: Rows up to which a product is a decode GEMV (tuning/search.py GEMV_MAX_M).
+_GEMV_MAX_M = 8
+
+
 @lru_cache(maxsize=4096)
-def _shipped(operation: str, dtype: torch.dtype, dims: tuple, device_index: int) -> KernelConfig | None:
+def _shipped(operation: str, dtype: torch.dtype, dims: tuple, layout: str,
+             device_index: int) -> KernelConfig | None:
     shipped = packaged_cache()
     if shipped is None:
         return None
-    problem = Problem.create(operation, dtype, **dict(dims))
+    problem = Problem.create(operation, dtype, layout=layout, **dict(dims))
     return shipped.get(problem, resolve_device_key(torch.device("cuda", device_index)))
 
 
-def shipped_config(operation: str, dtype: torch.dtype, device: torch.device, **dims: int) -> KernelConfig | None:
+def shipped_config(operation: str, dtype: torch.dtype, device: torch.device, *, layout: str = "",
+                   **dims: int) -> KernelConfig | None:
     """The packaged winner for this call's shape on ``device``, if one ships.
 
     What a kernel entry point runs when the caller passes no configuration
@@ -98,4 +114,4 @@ def shipped_config(operation: str, dtype: torch.dtype, device: torch.device, **d
     if device.type != "cuda" or min(dims.values()) < 1:
         return None
     index = device.index if device.index is not None else torch.cuda.current_device()
-    return _shipped(operation, dtype, tuple(dims.items()), index)
+    return _shipped(operation, dtype, tuple(dims.items()), layout, index)

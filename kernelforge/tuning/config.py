@@ -153,35 +153,56 @@ class KernelConfig(Mapping[str, int]):
         return "\n".join(f"{(k + ':').ljust(pad)} {self._index[k]:>4}" for k in ranked)
 
 
+#: Operand layouts a product's problem can name. ``""`` is B stored (K, N)
+#: row-major, the reference's only case; ``"bt"`` is B read k-contiguous, an
+#: ``nn.Linear`` weight passed as ``weight.t()``. The decode GEMV runs a
+#: different kernel for each (a column's k-run is contiguous only in the
+#: second), so their tuned configurations are kept apart.
+LAYOUTS = ("", "bt")
+_LAYOUT_OPERATIONS = ("matmul", "fused_linear")
+
+
 class Problem:
     """One workload: an operation over named dimensions in one dtype.
 
     Dimension names travel with the values (``M/N/K`` for products,
     ``rows/cols`` for row kernels, ``n`` for elementwise) because they become
-    parts of cache keys and database rows.
+    parts of cache keys and database rows. A product over k-contiguous B
+    carries ``layout="bt"``, which its keys show as a ``+bt`` suffix; every
+    other problem's keys are the reference's.
     """
 
-    __slots__ = ("operation", "dims", "dtype", "_key")
+    __slots__ = ("operation", "dims", "dtype", "layout", "_key")
 
-    def __init__(self, operation: str, dims: tuple[tuple[str, int], ...], dtype: torch.dtype):
+    def __init__(self, operation: str, dims: tuple[tuple[str, int], ...], dtype: torch.dtype,
+                 layout: str = ""):
+        if layout not in LAYOUTS:
+            raise ValueError(f"unknown operand layout {layout!r}; expected one of {LAYOUTS}")
+        if layout and operation not in _LAYOUT_OPERATIONS:
+            raise ValueError(f"{operation} has no operand layouts")
         object.__setattr__(self, "operation", operation)
         object.__setattr__(self, "dims", tuple((str(k), int(v)) for k, v in dims))
         object.__setattr__(self, "dtype", dtype)
-        object.__setattr__(self, "_key", (operation, self.dims, dtype))
+        object.__setattr__(self, "layout", layout)
+        object.__setattr__(self, "_key", (operation, self.dims, dtype, layout))
 
     def __setattr__(self, name: str, value: object) -> None:
         raise AttributeError("Problem is immutable")
 
     def __reduce__(self):
-        return (Problem, (self.operation, self.dims, self.dtype))
+        return (Problem, (self.operation, self.dims, self.dtype, self.layout))
 
     @classmethod
-    def create(cls, operation: str, dtype: str | torch.dtype, **dims: int) -> Problem:
+    def create(cls, operation: str, dtype: str | torch.dtype, *, layout: str = "",
+               **dims: int) -> Problem:
         bad = {k: v for k, v in dims.items() if isinstance(v, bool) or not isinstance(v, int) or v < 1}
         if bad:
             key, value = next(iter(bad.items()))
             raise ValueError(f"dimension {key!r} must be a positive int, got {value!r}")
-        return cls(operation, tuple(dims.items()), parse_dtype(dtype))
+        return cls(operation, tuple(dims.items()), parse_dtype(dtype), layout)
+
+    def with_layout(self, layout: str) -> Problem:
+        return Problem(self.operation, self.dims, self.dtype, layout)
 
     def __eq__(self, other: object) -> bool:
         if isinstance(other, Problem):
@@ -206,8 +227,9 @@ class Problem:
 
     @property
     def shape_key(self) -> str:
-        """Values in declaration order: ``2048x4096x4096``."""
-        return "x".join(map(str, (v for _, v in self.dims)))
+        """Values in declaration order: ``2048x4096x4096`` (``1x11008x4096+bt``)."""
+        key = "x".join(map(str, (v for _, v in self.dims)))
+        return f"{key}+{self.layout}" if self.layout else key
 
     @property
     def dtype_name(self) -> str:
@@ -225,8 +247,12 @@ class Problem:
         """``matmul M/N/K=2048 x 4096 x 4096 fp16``."""
         names = "/".join(name for name, _ in self.dims)
         values = " x ".join(str(v) for _, v in self.dims)
-        return f"{self.operation} {names}={values} {self.dtype_name}"
+        tail = ", B k-contiguous" if self.layout == "bt" else ""
+        return f"{self.operation} {names}={values} {self.dtype_name}{tail}"
 
     def as_dict(self) -> dict[str, Any]:
-        return {"operation": self.operation, "dims": self.dims_dict, "dtype": self.dtype_name,
-                "shape_key": self.shape_key}
+        out = {"operation": self.operation, "dims": self.dims_dict, "dtype": self.dtype_name,
+               "shape_key": self.shape_key}
+        if self.layout:
+            out["layout"] = self.layout
+        return out

@@ -395,6 +395,9 @@ class _GemmSpace(SearchSpace):
         dims = problem.dims_dict
         if config.get("GEMV"):
             lanes = config.get("LANES_PER_ROW", GEMV_DEFAULT_LANES_PER_ROW)
+            if problem.layout == "bt":
+                # gemv_dot: a wave load covers 64/lanes columns, a block num_warps of those.
+                return ceil_div(dims["N"], config["num_warps"] * (64 // lanes)) * config["SPLIT_K"]
             strip = lanes * (VECTOR_BYTES // problem.itemsize)
             return ceil_div(dims["N"], strip) * config["SPLIT_K"]
         tiles = ceil_div(dims["M"], config["BLOCK_M"]) * ceil_div(dims["N"], config["BLOCK_N"])
@@ -405,6 +408,8 @@ class _GemmSpace(SearchSpace):
         m, n, k = dims["M"], dims["N"], dims["K"]
         elem = itemsize(problem.dtype)
         if config.get("GEMV"):
+            if problem.layout == "bt":
+                return self._gemv_dot_reason(config, m, k, elem)
             return self._gemv_reason(config, m, k, elem)
 
         bm, bn = config["BLOCK_M"], config["BLOCK_N"]
@@ -474,6 +479,20 @@ class _GemmSpace(SearchSpace):
             )
         return None
 
+    def _gemv_dot_reason(self, config: KernelConfig, m: int, k: int, elem: int) -> str | None:
+        """gemv_dot (k-contiguous W): lanes split one column's k-run into 16-byte
+        vectors, so a slice needs at least one vector per lane."""
+        warps, split = config["num_warps"], config["SPLIT_K"]
+        lanes = config.get("LANES_PER_ROW", GEMV_DEFAULT_LANES_PER_ROW)
+        mr = next_power_of_2(m)
+        max_warps = 16 if mr == 4 else 8
+        if warps > max_warps:
+            return f"register pressure: {mr} rows of x allow at most {max_warps} waves, got {warps}"
+        slice_k = ceil_div(k, split)
+        if split > 1 and slice_k < lanes * (VECTOR_BYTES // elem):
+            return f"split-K slice too short: {slice_k} of K for {lanes} lanes of 16-byte vectors"
+        return None
+
     def priority(
         self, config: KernelConfig, problem: Problem, caps: DeviceCaps
     ) -> tuple[float, ...]:
@@ -495,6 +514,13 @@ class _GemmSpace(SearchSpace):
         """
         dims = problem.dims_dict
         programs = self.num_programs(config, problem)
+        if config.get("GEMV") and problem.layout == "bt":
+            # gemv_dot measured best with whole 64-lane columns and no split
+            # wherever that fills the CUs (1x11008x4096 bf16: 18.4 us against
+            # 32 us for the strip kernel's tuned configuration).
+            lanes = config.get("LANES_PER_ROW", GEMV_DEFAULT_LANES_PER_ROW)
+            return (0, -min(programs, caps.cu_count), config["SPLIT_K"], -lanes,
+                    abs(config["num_warps"] - 4))
         if config.get("GEMV"):
             waves = programs * config["num_warps"]
             lanes = config.get("LANES_PER_ROW", GEMV_DEFAULT_LANES_PER_ROW)

@@ -179,3 +179,52 @@ def test_exact_fp32_matmul_restores_flags():
         assert torch.backends.cuda.matmul.allow_tf32 is False
         assert torch.get_float32_matmul_precision() == "highest"
     assert (torch.backends.cuda.matmul.allow_tf32, torch.get_float32_matmul_precision()) == before
+
+
+def test_problem_layout_is_part_of_the_key_only_when_set():
+    import pickle
+
+    plain = Problem.create("matmul", "bf16", M=1, N=11008, K=4096)
+    bt = Problem.create("matmul", "bf16", layout="bt", M=1, N=11008, K=4096)
+    assert plain.cache_key == "matmul/bf16/1x11008x4096"  # the reference's key, unchanged
+    assert bt.cache_key == "matmul/bf16/1x11008x4096+bt"
+    assert bt != plain and hash(bt) != hash(plain)
+    assert pickle.loads(pickle.dumps(bt)) == bt
+    assert bt.with_layout("") == plain
+    assert "k-contiguous" in bt.describe() and bt.as_dict()["layout"] == "bt"
+    with pytest.raises(ValueError, match="layout"):
+        Problem.create("matmul", "fp16", layout="tt", M=1, N=2, K=3)
+    with pytest.raises(ValueError, match="no operand layouts"):
+        Problem.create("rmsnorm", "fp16", layout="bt", rows=1, cols=2)
+
+
+def test_decode_over_k_contiguous_weights_ranks_the_dot_kernel_shape_first():
+    """gemv_dot measured fastest with whole 64-lane columns and no split."""
+    from kernelforge.runtime.env import MI355X_CAPS
+    from kernelforge.tuning.search import search_space
+
+    bt = Problem.create("matmul", "bf16", layout="bt", M=1, N=11008, K=4096)
+    first = search_space("matmul").candidates(bt, MI355X_CAPS, max_candidates=1)[0]
+    assert (first["GEMV"], first["LANES_PER_ROW"], first["SPLIT_K"]) == (1, 64, 1)
+    plain = bt.with_layout("")
+    assert search_space("matmul").candidates(plain, MI355X_CAPS, max_candidates=1)[0] != first
+
+
+def test_select_config_borrows_row_major_winners_for_tiles_but_not_for_decode(tmp_path):
+    from kernelforge.kernels import get_operator
+    from kernelforge.runtime.dispatch import SOURCE_CACHE, SOURCE_DEFAULT, select_config
+    from kernelforge.tuning.cache import ConfigCache
+
+    cache = ConfigCache(tmp_path / "c.json")
+    op = get_operator("fused_linear")
+    tile = KernelConfig("fused_linear", BLOCK_M=128, BLOCK_N=128, BLOCK_K=64, GROUP_M=8, DIRECT=1,
+                        num_stages=3, num_warps=8)
+    gemv = KernelConfig("fused_linear", GEMV=1, LANES_PER_ROW=32, SPLIT_K=4, num_warps=8)
+    cache.put(Problem.create("fused_linear", "fp16", M=512, N=11008, K=4096), "cpu", tile)
+    cache.put(Problem.create("fused_linear", "fp16", M=1, N=11008, K=4096), "cpu", gemv)
+    big = select_config(op, Problem.create("fused_linear", "fp16", layout="bt", M=512, N=11008, K=4096),
+                        cache=cache, device="cpu", use_packaged=False)
+    assert (big.source, big.config) == (SOURCE_CACHE, tile)
+    decode = select_config(op, Problem.create("fused_linear", "fp16", layout="bt", M=1, N=11008, K=4096),
+                           cache=cache, device="cpu", use_packaged=False)
+    assert decode.source == SOURCE_DEFAULT and decode.config["LANES_PER_ROW"] == 64

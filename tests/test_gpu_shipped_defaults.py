@@ -80,3 +80,25 @@ def test_unshipped_shape_falls_back_to_the_heuristic():
     assert torch.equal(matmul(a, b), matmul(a, b, config=heuristic))
     empty = torch.empty(0, 64, dtype=torch.float16, device=DEV)
     assert matmul(empty, torch.randn(64, 32, dtype=torch.float16, device=DEV)).shape == (0, 32)
+
+
+def test_decode_over_nn_linear_weights_runs_its_own_winner(tmp_path):
+    """``x @ weight.t()`` is the dot-kernel layout: its shipped winner is keyed
+    ``+bt`` and differs from the row-major winner of the same shape."""
+    g = torch.Generator().manual_seed(8)
+    x = (torch.rand(1, 4096, generator=g) * 2 - 1).bfloat16().to(DEV)
+    weight = (torch.rand(11008, 4096, generator=g) * 2 - 1).bfloat16().to(DEV)
+    bt = _packaged_bt("matmul", torch.bfloat16, tmp_path, M=1, N=11008, K=4096)
+    row_major = _packaged("matmul", torch.bfloat16, tmp_path, M=1, N=11008, K=4096)
+    assert bt["LANES_PER_ROW"] == 64 and bt != row_major
+    assert torch.equal(matmul(x, weight.t()), matmul(x, weight.t(), config=bt))
+    bias = torch.randn(11008, generator=g).bfloat16().to(DEV)
+    fbt = _packaged_bt("fused_linear", torch.bfloat16, tmp_path, M=1, N=11008, K=4096)
+    assert torch.equal(fused_linear_gelu(x, weight.t(), bias), fused_linear_gelu(x, weight.t(), bias, config=fbt))
+
+
+def _packaged_bt(operation, dtype, tmp_path, **dims):
+    sel = select_config(get_operator(operation), Problem.create(operation, dtype, layout="bt", **dims),
+                        cache=ConfigCache(tmp_path / "empty_bt.json"), device=DEV)
+    assert sel.source == SOURCE_PACKAGED
+    return sel.config
