@@ -50,7 +50,10 @@ def build_problem(operation: str, args: argparse.Namespace) -> Problem:
     if operation not in _SHAPES:
         raise ValueError(f"unknown operation {operation!r}")
     dims = {dim: getattr(args, flag, None) or default for dim, flag, default in _SHAPES[operation]}
-    return Problem.create(operation, parse_dtype(args.dtype), **dims)
+    layout = "bt" if getattr(args, "b_layout", "kn") == "nk" else ""
+    if layout and operation not in ("matmul", "fused_linear"):
+        raise ValueError(f"--b-layout applies to matmul and fused_linear, not {operation}")
+    return Problem.create(operation, parse_dtype(args.dtype), layout=layout, **dims)
 
 
 def _heading(title: str) -> str:
@@ -172,6 +175,9 @@ def _shape_arguments(p: argparse.ArgumentParser) -> None:
     g.add_argument("--rows", type=int, help="rows (rmsnorm, softmax)")
     g.add_argument("--cols", type=int, help="row width (rmsnorm, softmax)")
     g.add_argument("--elements", type=int, help="element count (vector_add)")
+    g.add_argument("--b-layout", choices=("kn", "nk"), default="kn",
+                   help="how B is stored: kn = (K, N) row-major (default); nk = an nn.Linear "
+                        "weight (N, K), passed as weight.t() (matmul, fused_linear)")
 
 
 def _timing_arguments(p: argparse.ArgumentParser, warmup: int = 25, iterations: int = 200) -> None:

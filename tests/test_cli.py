@@ -122,3 +122,17 @@ def test_compare_runs_end_to_end(capsys):
     assert code == 0
     out = capsys.readouterr().out
     assert "kernelforge" in out and "torch_eager" in out and "GB/s" in out
+
+
+def test_b_layout_flag_names_the_k_contiguous_problem():
+    """``--b-layout nk`` tunes the nn.Linear-weight layout, keyed ``+bt``."""
+    import argparse
+
+    from kernelforge.cli.main import build_problem
+
+    args = argparse.Namespace(dtype="bf16", m=1, n=11008, k=4096, b_layout="nk")
+    assert build_problem("matmul", args).cache_key == "matmul/bf16/1x11008x4096+bt"
+    args.b_layout = "kn"
+    assert build_problem("matmul", args).cache_key == "matmul/bf16/1x11008x4096"
+    with pytest.raises(ValueError, match="b-layout"):
+        build_problem("rmsnorm", argparse.Namespace(dtype="fp32", rows=4, cols=8, b_layout="nk"))
