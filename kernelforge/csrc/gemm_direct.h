@@ -66,6 +66,28 @@ typedef __bf16 bf16x4_t __attribute__((__vector_size__(4 * sizeof(__bf16))));
 
 constexpr int kDirectBK = 64;
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// v_mfma_f32_32x32x16 on 16-bit inputs. Lane l holds A row l%32 (B column
+// l%32) at k 8*(l/32)..+7 of a 16-wide k step, and accumulator element v of
+// C row 8*(v/4) + 4*(l/32) + v%4, column l%32.
+template <typename T>
+struct Mma32;
+template <>
+struct Mma32<f16> {
+  __device__ __forceinline__ static void run(const u32x4& a, const u32x4& b, f32x16& c) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                               __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+template <>
+struct Mma32<bf16> {
+  __device__ __forceinline__ static void run(const u32x4& a, const u32x4& b, f32x16& c) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
 // 4 k-rows of one column from an n-contiguous LDS tile (see header comment).
 template <typename T>
 __device__ __forceinline__ uint64_t ds_read_tr4(const char* p);
@@ -170,13 +192,22 @@ struct DirectTile {
   static constexpr int WN = WaveGrid<WAVES, BM, BN>::WN;
   static constexpr int TM = BM / WM;
   static constexpr int TN = BN / WN;
-  static constexpr int FM = TM / 16;
-  static constexpr int FN = TN / 16;
+  // Fragment edge: 32x32x16 MFMAs for the 256x256 tile, whose 64x128 wave
+  // tiles hold 128 accumulators per lane either way but need half the
+  // fragment registers of 16x16 pieces; 16x16x32 everywhere else.
+  static constexpr int MF = (BM == 256 && BN == 256) ? 32 : 16;
+  static constexpr int FM = TM / MF;
+  static constexpr int FN = TN / MF;
+  static constexpr int kSteps = kDirectBK / (MF == 32 ? 16 : 32);  // MFMA k steps per slice
   // Byte sizes of one stage.
   static constexpr int kABytes = BM * BK * 2;
   static constexpr int kBBytes = BN * BK * 2;
   static constexpr int kStageBytes = kABytes + kBBytes;
-  static constexpr int kLdsBytes = STAGES * kStageBytes;  // static LDS
+  // Static LDS: the stages, or the staged C tile of the 32x32 path if larger.
+  static constexpr int kCStageBytes = BM * (BN + 8) * 2;
+  static constexpr int kLdsBytes = (MF == 32 && kCStageBytes > STAGES * kStageBytes)
+                                       ? kCStageBytes
+                                       : STAGES * kStageBytes;
   // 16-byte chunks per stage and DMA instructions per lane.
   static constexpr int kAIters = BM * BK / 8 / NT;
   static constexpr int kBIters = BN * BK / 8 / NT;
@@ -184,7 +215,8 @@ struct DirectTile {
   static constexpr int kBRowChunks = BN / 8;      // BLAYOUT 0: chunks per k-row of B
   static_assert(STAGES == 2 || STAGES == 3, "two or three LDS stages");
   static_assert((BM * BK / 8) % NT == 0 && (BN * BK / 8) % NT == 0, "DMA must tile the stage");
-  static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile must be whole 16x16 fragments");
+  static_assert(TM % MF == 0 && TN % MF == 0, "wave tile must be whole MFMA fragments");
+  static_assert(MF == 16 || STAGES == 2, "the 256x256 tile runs two stages");
   static_assert(2 * kPer < 64, "outstanding DMA must fit the vmcnt counter");
 };
 
@@ -271,9 +303,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   const int64_t ldb_b = (BLAYOUT == 0 ? args.ldb_k : args.ldb_n) * 2;  // bytes per B row
   const char* const b_tile = static_cast<const char*>(args.B) +
                              (BLAYOUT == 0 ? n0 * 2 + kt0 * BK * ldb_b : n0 * ldb_b + kt0 * BK * 2);
+  // The 256x256 tile computes its per-lane offsets from an opaque copy of the
+  // lane id, so the compiler cannot hoist the 64-bit row products out of the
+  // segment loop, where they would not fit its registers and spill.
+  int dtid = tid;
+  if constexpr (Tl::MF == 32) asm volatile("" : "+v"(dtid));
   constexpr int kRowsPerIter = NT / 8;  // k-contiguous rows (A, BLAYOUT 1) per DMA instruction
-  const int kr = tid >> 3;              // this lane's row within an instruction's rows
-  const int kc = swz_k(tid & 7, kr) * 8;  // its k within the slice; same for every j
+  const int kr = dtid >> 3;             // this lane's row within an instruction's rows
+  const int kc = swz_k(dtid & 7, kr) * 8;  // its k within the slice; same for every j
   uint32_t a_off[Tl::kAIters];
 #pragma unroll
   for (int j = 0; j < Tl::kAIters; ++j) {
@@ -282,20 +319,20 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
     a_off[j] = static_cast<uint32_t>(r * lda_b + kc * 2);
   }
   uint32_t b_off[Tl::kBIters];
-  int b_row[Tl::kBIters];  // BLAYOUT 0: k-row of the chunk within the slice
+  // BLAYOUT 0: k-row of chunk j within the slice. Recomputed where the
+  // partial last slice needs it rather than held through the K loop.
+  auto b_row = [&](int j) { return (j * NT + tid) / Tl::kBRowChunks; };
 #pragma unroll
   for (int j = 0; j < Tl::kBIters; ++j) {
-    const int q = j * NT + tid;
+    const int q = j * NT + dtid;
     if constexpr (BLAYOUT == 0) {
       const int r = q / Tl::kBRowChunks;
       int64_t col = swz_n<Tl::kBRowChunks>(q % Tl::kBRowChunks, r) * 8;
       col = (n0 + col < N) ? col : (N - 8 - n0);
-      b_row[j] = r;
       b_off[j] = static_cast<uint32_t>(r * ldb_b + col * 2);
     } else {
       int64_t r = j * kRowsPerIter + kr;
       r = (n0 + r < N) ? r : (N - 1 - n0);
-      b_row[j] = 0;
       b_off[j] = static_cast<uint32_t>(r * ldb_b + kc * 2);
     }
   }
@@ -332,8 +369,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
       const char* bb = b_tile + k0 * ldb_b;
 #pragma unroll
       for (int j = 0; j < Tl::kBIters; ++j) {
-        const int kb = b_row[j] < rem ? b_row[j] : rem - 1;
-        const uint32_t off = b_off[j] - static_cast<uint32_t>(b_row[j] * ldb_b) +
+        const int kb = b_row(j) < rem ? b_row(j) : rem - 1;
+        const uint32_t off = b_off[j] - static_cast<uint32_t>(b_row(j) * ldb_b) +
                              static_cast<uint32_t>(kb * ldb_b);
         dma16(bb, off, la + Tl::kABytes + j * NT * 16);
       }
@@ -359,7 +396,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
       if (kc >= rem) *reinterpret_cast<u32x4*>(stage + (j * NT + tid) * 16) = z;
 #pragma unroll
     for (int j = 0; j < Tl::kBIters; ++j) {
-      const int kk = BLAYOUT == 0 ? b_row[j] : kc;
+      const int kk = BLAYOUT == 0 ? b_row(j) : kc;
       if (kk >= rem) *reinterpret_cast<u32x4*>(stage + Tl::kABytes + (j * NT + tid) * 16) = z;
     }
   };
@@ -368,47 +405,69 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   // Tiles with 128 or more accumulator registers per lane (4 waves over 256x128
   // or 128x256) run one wave per SIMD, whose 512 registers exceed the 256
   // VGPRs: an operand in an AGPR lets the compiler put accumulators there.
-  if constexpr (FM * FN * 4 >= 128) asm volatile("" ::"a"(0.0f));
-  f32x4 acc[FM][FN];
+  // The 16x16x32 tiles (the 32x32x16 one holds its accumulators in VGPRs:
+  // the hint made the compiler split them 128/128 between the files and spill).
+  constexpr int MF = Tl::MF;
+  constexpr int kSteps = Tl::kSteps;
+  using AccT = std::conditional_t<MF == 32, f32x16, f32x4>;
+  if constexpr (MF == 16 && FM * FN * 4 >= 128) asm volatile("" ::"a"(0.0f));
+  AccT acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < FN; ++j) acc[i][j] = AccT{};
 
-  const int g = lane >> 4;   // lane group: k offset 8*g within a 32-wide step
-  const int li = lane & 15;  // row (A) / column (B) within a fragment
+  const int g = lane >> 4;   // 16x16x32: lane group, k offset 8*g within a 32-wide step
+  const int li = lane & 15;  // 16x16x32: row (A) / column (B) within a fragment
+  const int fr = MF == 32 ? (lane & 31) : li;  // the lane's row (A) / column (B) in a fragment
   // Stage-relative byte offsets of this lane's fragments for k step c. Rows
-  // i*16 apart share the swizzle, so fragment i adds i*16 rows as an immediate.
-  const int ar = wm * Tl::TM + li;
-  int a_frag[2];
-  int b_frag[2][FN];
+  // MF apart share the swizzle, so fragment i adds i*MF rows as an immediate.
+  const int ar = wm * Tl::TM + fr;
+  int a_frag[kSteps];
+  int b_frag[kSteps][FN];
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    a_frag[c] = ar * 128 + swz_k(c * 4 + g, ar) * 16;
+  for (int c = 0; c < kSteps; ++c) {
+    // 16-byte k chunk of the 64-wide slice: 16x16x32 lane groups take chunks
+    // 4c..4c+3, 32x32x16 lane halves chunks 2c and 2c+1.
+    const int kch = MF == 32 ? 2 * c + (lane >> 5) : c * 4 + g;
+    a_frag[c] = ar * 128 + swz_k(kch, ar) * 16;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       if constexpr (BLAYOUT == 0) {
-        const int col = wn * Tl::TN + j * 16 + (li & 3) * 4;
-        const int r0 = c * 32 + 8 * g + (li >> 2);  // rows r0 and r0 + 4 share the swizzle
+        // Transposing reads: a 16-lane group covers 16 columns and 4 k-rows
+        // per read; 32x32x16 groups alternate column halves, then k halves.
+        const int col = MF == 32 ? wn * Tl::TN + j * 32 + 16 * (g & 1) + (li & 3) * 4
+                                 : wn * Tl::TN + j * 16 + (li & 3) * 4;
+        const int r0 = MF == 32 ? c * 16 + 8 * (g >> 1) + (li >> 2)
+                                : c * 32 + 8 * g + (li >> 2);  // rows r0 and r0 + 4 share the swizzle
         b_frag[c][j] = Tl::kABytes + r0 * (BN * 2) + swz_n<Tl::kBRowChunks>(col >> 3, r0) * 16 + (col & 7) * 2;
       } else {
-        const int br = wn * Tl::TN + j * 16 + li;
-        b_frag[c][j] = Tl::kABytes + br * 128 + swz_k(c * 4 + g, br) * 16;
+        const int br = wn * Tl::TN + j * MF + fr;
+        b_frag[c][j] = Tl::kABytes + br * 128 + swz_k(kch, br) * 16;
       }
     }
   }
+  // B offset of fragment j at k step c. On the 32x32 path the swizzles make
+  // the steps constant: n-contiguous rows 16 apart share the n-swizzle (the
+  // k steps differ by 16 rows), k-contiguous rows 32 apart the k one (the
+  // fragments differ by 32 rows), so one offset register serves each.
+  auto bfrag_off = [&](int c, int j) -> int {
+    if constexpr (MF == 32 && BLAYOUT == 0) return b_frag[0][j] + c * 16 * BN * 2;
+    else if constexpr (MF == 32) return b_frag[c][0] + j * 32 * 128;
+    else return b_frag[c][j];
+  };
   auto load_frags = [&](const char* S, int c, u32x4 (&af)[FM], u32x4 (&bf)[FN]) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const u32x4*>(S + a_frag[c] + i * 16 * 128);
+    for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const u32x4*>(S + a_frag[c] + i * MF * 128);
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       if constexpr (BLAYOUT == 0) {
-        const uint64_t lo = ds_read_tr4<T>(S + b_frag[c][j]);
-        const uint64_t hi = ds_read_tr4<T>(S + b_frag[c][j] + 4 * BN * 2);
+        const uint64_t lo = ds_read_tr4<T>(S + bfrag_off(c, j));
+        const uint64_t hi = ds_read_tr4<T>(S + bfrag_off(c, j) + 4 * BN * 2);
         bf[j] = u32x4{static_cast<uint32_t>(lo), static_cast<uint32_t>(lo >> 32),
                       static_cast<uint32_t>(hi), static_cast<uint32_t>(hi >> 32)};
       } else {
-        bf[j] = *reinterpret_cast<const u32x4*>(S + b_frag[c][j]);
+        bf[j] = *reinterpret_cast<const u32x4*>(S + bfrag_off(c, j));
       }
     }
   };
@@ -416,7 +475,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) Mma<T>::run(af[i], bf[j], acc[i][j]);
+      for (int j = 0; j < FN; ++j) {
+        if constexpr (MF == 32)
+          Mma32<T>::run(af[i], bf[j], acc[i][j]);
+        else
+          Mma<T>::run(af[i], bf[j], acc[i][j]);
+      }
   };
   // Both 32-wide k steps of a slice are read and multiplied before its
   // barrier. The scheduling groups pin the order: step 0's reads, then step
@@ -430,21 +494,26 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   constexpr int kReads = FM + (BLAYOUT == 0 ? 2 : 1) * FN;  // LDS reads per k step
   constexpr int kMfma = FM * FN;                           // MFMAs per k step
   constexpr int kPairs = kReads < kMfma ? kReads : kMfma;
+  // The 32x32x16 tile runs four 16-wide k steps per slice the same way:
+  // step s+1's reads alternate with step s's MFMAs.
   auto compute = [&](const char* S) {
-    u32x4 a0[FM], b0[FN], a1[FM], b1[FN];
-    load_frags(S, 0, a0, b0);
-    load_frags(S, 1, a1, b1);
-    mma_all(a0, b0);
-    mma_all(a1, b1);
+    u32x4 fa[kSteps][FM], fb[kSteps][FN];
+#pragma unroll
+    for (int c = 0; c < kSteps; ++c) load_frags(S, c, fa[c], fb[c]);
+#pragma unroll
+    for (int c = 0; c < kSteps; ++c) mma_all(fa[c], fb[c]);
     __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // step 0 reads
 #pragma unroll
-    for (int q = 0; q < kPairs; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one step-1 read
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one step-0 MFMA
+    for (int c = 0; c + 1 < kSteps; ++c) {
+#pragma unroll
+      for (int q = 0; q < kPairs; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one read of step c+1
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA of step c
+      }
+      if constexpr (kMfma > kPairs) __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kPairs, 0);
+      if constexpr (kReads > kPairs) __builtin_amdgcn_sched_group_barrier(0x100, kReads - kPairs, 0);
     }
-    if constexpr (kMfma > kPairs) __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kPairs, 0);
-    if constexpr (kReads > kPairs) __builtin_amdgcn_sched_group_barrier(0x100, kReads - kPairs, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, kMfma, 0);  // step 1 MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x008, kMfma, 0);  // the last step's MFMAs
   };
 
   // ---- main loop ------------------------------------------------------------------
@@ -535,9 +604,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
     // the only ordering needed is that every lane's stores have completed
     // (vmcnt(0), then the workgroup barrier) before the ticket is taken.
     // Program q keeps two partial slots: 2q for its first segment, 2q + 1
-    // for its last (middle segments are whole tiles). Fragment (i, j) of lane
-    // tid is the 16 bytes at ((i*FN + j)*NT + tid)*16 of a slot.
+    // for its last (middle segments are whole tiles). Part p (16 bytes) of
+    // fragment (i, j) of lane tid is at (((i*FN + j)*kParts + p)*NT + tid)*16
+    // of a slot; a fragment is one part (16x16) or four (32x32).
     constexpr int kTileFloats = BM * BN;
+    constexpr int kParts = static_cast<int>(sizeof(AccT)) / 16;
     const int64_t st = tile - full;  // index among the split tiles
     auto slot = [&](int64_t q, bool first) {
       return tile_rsrc(args.ws + (2 * q + (first ? 0 : 1)) * kTileFloats, kTileFloats * 4);
@@ -547,8 +618,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), mine,
-                                               ((i * FN + j) * NT + tid) * 16, 0, kCachePolicySc1);
+#pragma unroll
+        for (int pp = 0; pp < kParts; ++pp) {
+          const f32x4 part = {acc[i][j][4 * pp], acc[i][j][4 * pp + 1], acc[i][j][4 * pp + 2],
+                              acc[i][j][4 * pp + 3]};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, part), mine,
+                                                 (((i * FN + j) * kParts + pp) * NT + tid) * 16, 0,
+                                                 kCachePolicySc1);
+        }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     wait_vm<0>();  // this lane's partial stores are done
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -570,20 +647,35 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < FN; ++j) acc[i][j] = AccT{};
     for (int64_t q = q0; q <= q1; ++q) {
       const __amdgpu_buffer_rsrc_t src = slot(q, (q * I / P) / nk_all == st);
-      u32x4 pv[FM][FN];  // all of segment q's loads in flight before the first add
+      // A segment's loads are in flight together before the first add: all of
+      // them for 16x16 fragments, one fragment row at a time for 32x32 ones
+      // (all at once would need another 128 registers per lane).
+      constexpr int kRowsInFlight = kParts == 1 ? FM : 1;
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+      for (int i0 = 0; i0 < FM; i0 += kRowsInFlight) {
+        u32x4 pv[kRowsInFlight][FN][kParts];
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
-          pv[i][j] = __builtin_amdgcn_raw_buffer_load_b128(src, ((i * FN + j) * NT + tid) * 16, 0,
-                                                           kCachePolicySc1);
+        for (int di = 0; di < kRowsInFlight; ++di)
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+          for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] += __builtin_bit_cast(f32x4, pv[i][j]);
+            for (int pp = 0; pp < kParts; ++pp)
+              pv[di][j][pp] = __builtin_amdgcn_raw_buffer_load_b128(
+                  src, ((((i0 + di) * FN + j) * kParts + pp) * NT + tid) * 16, 0, kCachePolicySc1);
+#pragma unroll
+        for (int di = 0; di < kRowsInFlight; ++di)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int pp = 0; pp < kParts; ++pp) {
+              const f32x4 part = __builtin_bit_cast(f32x4, pv[di][j][pp]);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc[i0 + di][j][4 * pp + e] += part[e];
+            }
+      }
     }
     if (tid == 0) __hip_atomic_store(&args.tickets[st], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -592,7 +684,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   // Opaque copies of the tile origin: no epilogue address can be computed
   // ahead of the K loop, where it would hold registers for the whole loop.
   int64_t em0 = m0, en0 = n0;
-  int eli = li, eg = g, etid = tid;
+  // The lane's column in a fragment and its row group: accumulator element e
+  // is fragment row 4*eg + e (16x16) or 8*(e/4) + 4*eg + e%4 (32x32).
+  int eli = fr, eg = MF == 32 ? (lane >> 5) : g, etid = tid;
+  constexpr int kAccN = MF == 32 ? 16 : 4;
+  auto frag_row = [&](int e) { return MF == 32 ? 8 * (e >> 2) + 4 * eg + (e & 3) : 4 * eg + e; };
   asm volatile("" : "+s"(em0), "+s"(en0), "+v"(eli), "+v"(eg), "+v"(etid));
   T* __restrict__ C = static_cast<T*>(args.C);
   const T* __restrict__ bias = static_cast<const T*>(args.bias);
@@ -610,16 +706,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
     T* const ct = reinterpret_cast<T*>(lds);
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      const int cl = wn * Tl::TN + j * 16 + eli;
+      const int cl = wn * Tl::TN + j * MF + eli;
       const int64_t col = en0 + cl;
       const float bcol = (gelu && col < N) ? to_f32(bias[col]) : 0.f;
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < kAccN; ++r) {
           float v = acc[i][j][r];
           if (gelu) v = gelu_tanh(v + bcol);
-          ct[(wm * Tl::TM + i * 16 + eg * 4 + r) * kPitch + cl] = from_f32<T>(v);
+          ct[(wm * Tl::TM + i * MF + frag_row(r)) * kPitch + cl] = from_f32<T>(v);
         }
     }
     __syncthreads();
@@ -641,14 +737,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   }
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
-    const int64_t col = en0 + wn * Tl::TN + j * 16 + eli;
+    const int64_t col = en0 + wn * Tl::TN + j * MF + eli;
     if (col >= N) continue;
     const float bcol = gelu ? to_f32(bias[col]) : 0.f;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t row = em0 + wm * Tl::TM + i * 16 + eg * 4 + r;
+      for (int r = 0; r < kAccN; ++r) {
+        const int64_t row = em0 + wm * Tl::TM + i * MF + frag_row(r);
         if (row >= M) continue;
         float v = acc[i][j][r];
         if (gelu) v = gelu_tanh(v + bcol);

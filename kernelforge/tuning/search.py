@@ -42,6 +42,17 @@ DEFAULT_MAX_CANDIDATES = 48
 #: v_mfma_f32_16x16x4_f32 all produce 16x16 fp32 tiles.
 MFMA_TILE = 16
 
+
+def mfma_fragment_edge(block_m: int, block_n: int, *, direct: int = 0) -> int:
+    """Edge of the MFMA output fragments a tile is built from (gemm_direct.h DirectTile::MF).
+
+    The direct pipeline's 256x256 tile multiplies with v_mfma_f32_32x32x16:
+    its 64x128 wave tiles hold 128 accumulators per lane with either shape,
+    but 32x32 fragments take half the fragment registers. Every other tile
+    uses 16x16 fragments.
+    """
+    return 32 if direct and block_m == 256 and block_n == 256 else MFMA_TILE
+
 #: k consumed per MFMA step per fragment: 4 lane groups x 16 bytes of operand.
 MFMA_K = {2: 32, 4: 16}
 
@@ -234,7 +245,8 @@ def gemm_tile_regs(
     lanes = waves * 64
     wm, wn = wave_grid(waves, block_m, block_n)
     acc = block_m * block_n // lanes
-    frags = 4 * (block_m // wm // MFMA_TILE + block_n // wn // MFMA_TILE) * (2 if direct else 1)
+    edge = mfma_fragment_edge(block_m, block_n, direct=direct)
+    frags = 4 * (block_m // wm // edge + block_n // wn // edge) * (2 if direct else 1)
     staged = 0 if direct else 4 * ceil_div((block_m + block_n) * block_k * elem, VECTOR_BYTES * lanes)
     return {"acc": acc, "frags": frags, "staged": staged, "total": acc + frags + staged}
 
@@ -246,6 +258,18 @@ DIRECT_BLOCK_K = 64
 def gemm_direct_lds_bytes(block_m: int, block_n: int, stages: int) -> int:
     """LDS of the direct pipeline: dense (unpadded, swizzled) 16-bit stages."""
     return stages * (block_m + block_n) * DIRECT_BLOCK_K * 2
+
+
+def gemm_direct_static_lds_bytes(block_m: int, block_n: int, stages: int) -> int:
+    """The direct kernel's static LDS (gemm_direct.h DirectTile::kLdsBytes).
+
+    The stages, except on the 32x32x16 path, whose staged C tile (rows of
+    BLOCK_N + 8 16-bit elements) is larger than its two stages and sets the size.
+    """
+    lds = gemm_direct_lds_bytes(block_m, block_n, stages)
+    if mfma_fragment_edge(block_m, block_n, direct=1) == 32:
+        lds = max(lds, block_m * (block_n + 8) * 2)
+    return lds
 
 
 def gemm_direct_reason(

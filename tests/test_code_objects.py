@@ -17,8 +17,9 @@ from codeobj import load_kernels
 from kernelforge.runtime import hip
 from kernelforge.tuning.search import (
     REGISTER_FILE_PER_LANE,
-    gemm_direct_lds_bytes,
+    gemm_direct_static_lds_bytes,
     gemm_instantiations,
+    mfma_fragment_edge,
 )
 
 
@@ -61,13 +62,23 @@ def test_register_use_stays_in_the_file(kernels):
         assert k.vgprs + k.agprs <= REGISTER_FILE_PER_LANE, name
 
 
-def test_mfma_instructions_match_the_dtype(kernels):
+def test_mfma_instructions_match_the_dtype_and_tile(kernels):
     expect = {"fp16": "v_mfma_f32_16x16x32_f16", "bf16": "v_mfma_f32_16x16x32_bf16",
               "fp32": "v_mfma_f32_16x16x4_f32"}
+    wide = {"fp16": "v_mfma_f32_32x32x16_f16", "bf16": "v_mfma_f32_32x32x16_bf16"}
+    seen_wide = 0
     for name, k in kernels.items():
         p = _gemm_params(name)
-        if p:
-            assert k.count(expect[p[1]]) > 0, name
+        if not p:
+            continue
+        direct, dtype, ints = p
+        if direct and mfma_fragment_edge(ints[0], ints[1], direct=1) == 32:
+            # 256x256: 64x128 wave tiles of 32x32x16 products, 4 k steps x 8 per slice
+            assert k.count(wide[dtype]) > 0 and k.count(expect[dtype]) == 0, name
+            seen_wide += 1
+        else:
+            assert k.count(expect[dtype]) > 0, name
+    assert seen_wide == 2 * 2  # fp16, bf16 x both B layouts
 
 
 def test_direct_kernels_use_dma_and_transposing_reads(kernels):
@@ -80,8 +91,9 @@ def test_direct_kernels_use_dma_and_transposing_reads(kernels):
         direct, dtype, (bm, bn, waves, blayout, stages) = p
         assert k.count("global_load_lds_dwordx4") > 0, name
         assert k.count("ds_read_b64_tr_b16") > 0 if blayout == 0 else True, name
-        # Static LDS = the search space's model of the dense stages, <= 160 KiB.
-        assert k.group_bytes == gemm_direct_lds_bytes(bm, bn, stages) <= 160 * 1024, name
+        # Static LDS = the search space's model of the dense stages (or the
+        # 256x256 tile's staged C), <= 160 KiB.
+        assert k.group_bytes == gemm_direct_static_lds_bytes(bm, bn, stages) <= 160 * 1024, name
     assert seen > 0
 
 

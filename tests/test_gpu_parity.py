@@ -168,6 +168,7 @@ _TILES = [
     (128, 256, 64, 8, 1, 3),
     (128, 256, 64, 4, 1, 3),
     (256, 64, 64, 8, 1, 3),
+    (256, 256, 64, 8, 1, 2),  # 32x32x16 fragments
 ]
 
 
@@ -245,6 +246,27 @@ def test_fused_linear_transposed_weight():
     bias = _randn(n, dtype=torch.float16, seed=3)
     out = fused_linear_gelu(x.to(DEV), weight.to(DEV).t(), bias.to(DEV))
     _gate(ops.linear_gelu_ref(x, weight.t(), bias), out, torch.float16, "fused weight.t()")
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16), ids=("fp16", "bf16"))
+@pytest.mark.parametrize("layout", ("nn", "nt"))
+@pytest.mark.parametrize("split", (1, 2, 3))
+@pytest.mark.parametrize("m,n,k", [(300, 520, 264), (1000, 1032, 1000), (512, 768, 4096)])
+def test_fused_linear_on_the_32x32_tile(dtype, layout, split, m, n, k):
+    """The 256x256 tile's epilogue maps accumulator element e of a 32x32 fragment
+    to row 8*(e/4) + 4*(lane/32) + e%4; bias + GELU run on it unsplit and on the
+    sum of split-K partial tiles (four 16-byte parts per fragment)."""
+    from kernelforge.kernels.fused_linear import fused_linear_gelu
+
+    x = _randn(m, k, dtype=dtype, seed=m + 1)
+    w = _randn(k, n, dtype=dtype, seed=n + 2, scale=k**-0.5)
+    bias = _randn(n, dtype=dtype, seed=9)
+    dw = w.to(DEV) if layout == "nn" else w.t().contiguous().to(DEV).t()
+    extra = {"SPLIT_K": split} if split > 1 else {}
+    cfg = KernelConfig("fused_linear", BLOCK_M=256, BLOCK_N=256, BLOCK_K=64, GROUP_M=4, DIRECT=1,
+                       num_warps=8, num_stages=2, **extra)
+    out = fused_linear_gelu(x.to(DEV), dw, bias.to(DEV), config=cfg)
+    _gate(ops.linear_gelu_ref(x, w, bias), out, dtype, f"{cfg} {layout} {m}x{n}x{k}")
 
 
 def test_fused_linear_identity_weight_traces_gelu():

@@ -64,8 +64,10 @@ def _split_call(da, db, bias, bm, bn, waves, split, *, stages=3, out_dtype=None)
     return inside, bool(torch.isnan(host[guard]).all())
 
 
-# (BLOCK_M, BLOCK_N, waves)
-_TILES = [(32, 64, 4), (64, 64, 4), (32, 128, 4), (64, 128, 8), (128, 128, 8), (256, 128, 8)]
+# (BLOCK_M, BLOCK_N, waves[, stages]); the 256x256 tile (32x32x16 fragments,
+# four 16-byte parts per fragment in a partial tile) has two stages only.
+_TILES = [(32, 64, 4), (64, 64, 4), (32, 128, 4), (64, 128, 8), (128, 128, 8), (256, 128, 8),
+          (256, 256, 8, 2)]
 
 
 @pytest.mark.parametrize("tile", _TILES, ids=lambda t: "x".join(map(str, t)))
@@ -78,10 +80,11 @@ def test_split_k_matches_the_oracle(tile, split, m, n, k):
     """Shapes with M/N edges, K tails (K % 64 != 0), programs whose k-range is
     short or empty (K=128 at split 3..16 leaves programs with no slice), and
     split counts that do not divide the slice count."""
-    bm, bn, w = tile
+    bm, bn, w = tile[:3]
+    stages = tile[3] if len(tile) > 3 else 3
     a = _randn(m, k, dtype=torch.float16, seed=m + k)
     b = _randn(k, n, dtype=torch.float16, seed=n + split, scale=k**-0.5)
-    out, guard = _split_call(a.to(DEV), b.to(DEV), None, bm, bn, w, split)
+    out, guard = _split_call(a.to(DEV), b.to(DEV), None, bm, bn, w, split, stages=stages)
     assert guard, "split-K wrote outside C"
     assert torch.isfinite(out).all(), "a tile was never finished"
     _gate(ops.matmul_ref(a, b), out, torch.float16, f"{tile} split {split} {m}x{n}x{k}")

@@ -29,6 +29,8 @@ from kernelforge.tuning.search import (
     gemm_instantiation_reason,
     gemm_instantiations,
     gemm_lds_bytes,
+    gemm_tile_regs,
+    mfma_fragment_edge,
     next_power_of_2,
     search_space,
 )
@@ -108,13 +110,13 @@ def test_register_rules_follow_the_per_lane_budget():
     assert "register pressure" in gemm_instantiation_reason(256, 256, 64, 4, 2, 2, MI355X_CAPS)
     # 8 waves: two per SIMD, 256 registers per lane less a 64-register reserve.
     # The register-staged pipeline needs 128 acc + 48 fragment + 32 staging
-    # registers and does not fit; the direct pipeline stages nothing in
-    # registers but carries a second k step of fragments (128 + 2*48), which
-    # does not fit either. At 256x128 it does: 64 acc + 2*32 fragments.
+    # registers and does not fit. The direct pipeline stages nothing in
+    # registers but carries a second k step of fragments: in 16x16 pieces
+    # (128 + 2*48) it would not fit, and its 256x256 tile takes 32x32 pieces
+    # (128 + 2*24). At 256x128: 64 acc + 2*32 fragments.
     reason = gemm_instantiation_reason(256, 256, 64, 8, 2, 2, MI355X_CAPS)
     assert reason.startswith("register file") and "8 waves" in reason
-    reason = gemm_instantiation_reason(256, 256, 64, 8, 2, 2, MI355X_CAPS, direct=1)
-    assert reason.startswith("register file")
+    assert gemm_instantiation_reason(256, 256, 64, 8, 2, 2, MI355X_CAPS, direct=1) is None
     assert gemm_instantiation_reason(256, 128, 64, 8, 3, 2, MI355X_CAPS, direct=1) is None
 
 
@@ -278,10 +280,26 @@ def test_space_rejects_mismatched_problem():
     assert isinstance(search_space("vector_add"), VectorAddSearchSpace)
 
 
+def test_the_256x256_tile_fits_only_with_32x32_fragments():
+    # 64x128 wave tiles hold 128 accumulators per lane either way; the
+    # fragments of two k steps take 96 registers in 16x16 pieces (224 in all,
+    # over the 192 a tile may use at two waves per SIMD) and 48 in 32x32 pieces.
+    assert mfma_fragment_edge(256, 256, direct=1) == 32
+    assert mfma_fragment_edge(256, 256, direct=0) == 16
+    assert mfma_fragment_edge(128, 256, direct=1) == mfma_fragment_edge(256, 128, direct=1) == 16
+    assert gemm_tile_regs(256, 256, 64, 8, 2, direct=1) == {"acc": 128, "frags": 48, "staged": 0,
+                                                            "total": 176}
+    assert gemm_tile_regs(128, 256, 64, 8, 2, direct=1)["total"] == 64 + 64
+    assert gemm_instantiation_reason(256, 256, 64, 8, 2, 2, MI355X_CAPS, direct=1) is None
+    assert "LDS" in gemm_instantiation_reason(256, 256, 64, 8, 3, 2, MI355X_CAPS, direct=1)
+
+
 def test_instantiation_list_is_the_rule_filtered_grid():
     staged = gemm_instantiations(MI355X_CAPS)
     direct = gemm_instantiations(MI355X_CAPS, direct=1)
-    assert len(staged[2]) == 59 and len(staged[4]) == 80 and len(direct[2]) == 38
+    assert len(staged[2]) == 59 and len(staged[4]) == 80 and len(direct[2]) == 39
+    # The one 32x32x16 tile: 256x256 on eight waves, two 64 KiB stages.
+    assert [t for t in direct[2] if t[0] == t[1] == 256] == [(256, 256, 64, 8, 2)]
     assert direct[4] == [] and all(t[2] == 64 for t in direct[2])
     for elem, tiles in staged.items():
         for bm, bn, bk, w, s in tiles:
