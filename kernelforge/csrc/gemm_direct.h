@@ -698,6 +698,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   // pieces: 8 stores per lane for a 256x128 tile instead of 64 two-byte
   // ones, whose per-lane addressing held the tile's last round back
   // (4096x11008x4096: 387 -> 354 us). Other layouts store element by element.
+  // The row pieces are stored with the non-temporal policy: C is written once
+  // and not read back by this launch. Measured against plain stores, same
+  // outputs (flushed event medians): 2048x4096x4096 at 256x128 68.8 against
+  // 70.6 us, 4096x11008x4096 unsplit 360.7 against 371.4 us, 2048x11008x4096
+  // 187.8 against 190.9 us; level at 128x256 on 2048x4096x4096.
   constexpr int kPitch = BN + 8;  // elements per LDS row of the staged C: 16 bytes of padding
   constexpr bool kCFits = BM * kPitch * 2 <= Tl::kLdsBytes;
   const bool stage_c = kCFits && args.ldc_n == 1 && (args.ldc_m * 2) % 16 == 0 &&
@@ -727,7 +732,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
       const T* src = ct + rl * kPitch + cl;
       T* dst = C + row * args.ldc_m + col;
       if (col + 8 <= N) {
-        *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
+        __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(src), reinterpret_cast<u32x4*>(dst));
       } else {
         for (int e = 0; e < 8 && col + e < N; ++e) dst[e] = src[e];
       }
