@@ -25,6 +25,12 @@ launch cost but keeps the dependency drain between consecutive kernels and
 the clock the GPU holds under sustained load. Each replay's outputs are
 checked bitwise against the eager outputs.
 
+The torch comparators (hipBLASLt, the unfused matmul + bias + GELU, torch's
+GEMV, ``a + b``, eager RMSNorm) are timed the same way but alternating step by
+step with the kernel they are compared to (``interleaved_us`` is that
+kernel's mean in the same run), so a ratio of the two is not skewed by the
+clock rising or falling between two runs.
+
 Each configuration's output is checked against torch on the same device with
 the reference's gate before it is timed. The CPU baseline is the oracle
 (oracle/ops.py, torch eager in fp32) timed on the host cores on a bounded
@@ -75,6 +81,36 @@ def _time_flushed(fn, steps: int, warmup: int, flush) -> list[float]:
         end[i].record()
     torch.cuda.synchronize()
     return [start[i].elapsed_time(end[i]) for i in range(steps)]
+
+
+def _time_interleaved(ours, theirs, steps: int, warmup: int, flush) -> tuple[list[float], list[float]]:
+    """The reference's per-step method for a kernel and its torch comparator, the
+    two alternating step by step (ms per step of each).
+
+    Timed one after the other, the second would run further into the clock ramp
+    that sustained MFMA load causes on this board (a fused-linear launch takes
+    400+ us early in a process and 340 us once the clock settles), which biases
+    a ratio of the two; alternating gives both the same clock.
+    """
+    import torch
+
+    for _ in range(warmup):
+        ours()
+        theirs()
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    for i in range(steps):
+        flush.flush()
+        ev[i][0].record()
+        ours()
+        ev[i][1].record()
+        flush.flush()
+        ev[i][2].record()
+        theirs()
+        ev[i][3].record()
+    torch.cuda.synchronize()
+    return ([ev[i][0].elapsed_time(ev[i][1]) for i in range(steps)],
+            [ev[i][2].elapsed_time(ev[i][3]) for i in range(steps)])
 
 
 def _time_graph(fns, steps: int, warmup: int, flush):
@@ -254,6 +290,37 @@ def main(argv: list[str] | None = None) -> int:
     hbm = caps.peak_hbm_gbps
     f16_peak = caps.peak_fp16_tflops
 
+    # --- inputs: every configuration's seeded data, in HBM before anything is timed --
+    # Generating a configuration's inputs on the host right before timing it would
+    # leave the GPU idle for hundreds of milliseconds, and the first launches after
+    # an idle period run at a lower clock while it ramps back up (measured on the
+    # fused linear: 400-450 us for the first 10-20 launches, 340 us after).
+    x = torch.randn(4096, 4096, generator=g)
+    gamma = 1.0 + 0.1 * torch.randn(4096, generator=g)
+    dx, dgamma = x.to(dev), gamma.to(dev)
+    soft = {}
+    for cols in (4096, 11008):
+        s = 3.0 * torch.randn(8192, cols, generator=g)
+        s[torch.randperm(8192, generator=g)[:82]] += 60.0
+        soft[cols] = s.to(torch.float16).to(dev)
+        del s
+    M, N, K = 2048, 4096, 4096
+    a = (torch.randn(M, K, generator=g) / K**0.5).to(torch.float16).to(dev)
+    b = (torch.randn(K, N, generator=g) / K**0.5).to(torch.float16).to(dev)
+    FM, FN, FK = 4096, 11008, 4096
+    fx = (torch.randn(FM, FK, generator=g) / FK**0.5).to(torch.float16).to(dev)
+    fw = (torch.randn(FK, FN, generator=g) / FK**0.5).to(torch.float16).to(dev)
+    fb = (0.02 * torch.randn(FN, generator=g)).to(torch.float16).to(dev)
+    vx = (torch.rand(1, 4096, generator=g) * 2 - 1).to(torch.bfloat16).to(dev)
+    vw = (torch.rand(4096, 11008, generator=g) * 2 - 1).to(torch.bfloat16).to(dev)
+    VN = 1 << 26
+    va = torch.randn(VN, generator=g).to(dev)
+    vb = torch.randn(VN, generator=g).to(dev)
+    WR, WC = 4096, 32768
+    wx = torch.randn(WR, WC, generator=g).to(torch.float16).to(dev)
+    wg = (1.0 + 0.1 * torch.randn(WC, generator=g)).to(torch.float16).to(dev)
+    torch.cuda.synchronize()
+
     # --- calibration: a plain device-to-device copy of 1 GiB (read + write) -----
     src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
     dst = [torch.empty_like(src) for _ in range(2)]
@@ -262,9 +329,6 @@ def main(argv: list[str] | None = None) -> int:
     del src, dst
 
     # --- config 1: RMSNorm fp32 [4096,4096], eps=1e-6 ----------------------------
-    x = torch.randn(4096, 4096, generator=g)
-    gamma = 1.0 + 0.1 * torch.randn(4096, generator=g)
-    dx, dgamma = x.to(dev), gamma.to(dev)
     cfg, src = pick("rmsnorm", "fp32", rows=4096, cols=4096)
     assert_verified(rmsnorm_reference(dx, dgamma, eps=1e-6),
                     rmsnorm(dx, dgamma, eps=1e-6, config=cfg), context="rmsnorm config 1")
@@ -277,9 +341,7 @@ def main(argv: list[str] | None = None) -> int:
 
     # --- config 2: softmax fp16 [8192,4096] and [8192,11008], 1% rows +60 ---------
     for cols in (4096, 11008):
-        s = 3.0 * torch.randn(8192, cols, generator=g)
-        s[torch.randperm(8192, generator=g)[:82]] += 60.0
-        ds = s.to(torch.float16).to(dev)
+        ds = soft.pop(cols)
         cfg, src = pick("softmax", "fp16", rows=8192, cols=cols)
         out = softmax(ds, config=cfg)
         assert torch.isfinite(out).all()
@@ -290,12 +352,9 @@ def main(argv: list[str] | None = None) -> int:
         record(f"softmax_fp16_8192x{cols}",
                [lambda c=c, cfg=cfg: softmax(c[0], config=cfg) for c in cp],
                work, "GB/s", hbm, src)
-        del ds, s, cp, out
+        del ds, cp, out
 
     # --- config 3: GEMM fp16 2048x4096x4096 (headline) -----------------------------
-    M, N, K = 2048, 4096, 4096
-    a = (torch.randn(M, K, generator=g) / K**0.5).to(torch.float16).to(dev)
-    b = (torch.randn(K, N, generator=g) / K**0.5).to(torch.float16).to(dev)
     gcfg, src = pick("matmul", "fp16", M=M, N=N, K=K)
     with exact_fp32_matmul():
         assert_verified(torch.matmul(a.float(), b.float()), matmul(a, b, config=gcfg),
@@ -304,17 +363,16 @@ def main(argv: list[str] | None = None) -> int:
     gemm = record("gemm_fp16_2048x4096x4096",
                   [lambda c=c: matmul(c[0], c[1], config=gcfg) for c in cp],
                   metrics.matmul_flops(M, N, K), "TFLOP/s", f16_peak, src)
-    tg = _time_flushed(lambda: torch.matmul(a, b), steps, warmup, flush)
+    mine, tg = _time_interleaved(lambda: matmul(a, b, config=gcfg), lambda: torch.matmul(a, b),
+                                 steps, warmup, flush)
     gemm["torch_hipblaslt_tflops"] = metrics.matmul_flops(M, N, K) / (np.mean(tg) * 1e-3) / 1e12
+    gemm["interleaved_us"] = float(np.mean(mine)) * 1e3
+    gemm["speedup_vs_hipblaslt"] = float(np.mean(tg)) / float(np.mean(mine))
     ms, _ = (float("nan"), 0.0) if args.no_sustained else _time_graph([lambda c=c: torch.matmul(c[0], c[1]) for c in cp], steps, warmup, flush)
     gemm["torch_hipblaslt_sustained_tflops"] = metrics.matmul_flops(M, N, K) / (ms * 1e-3) / 1e12
     del cp
 
     # --- config 4: fused linear fp16 4096x11008x4096 + bias + GELU(tanh) -----------
-    FM, FN, FK = 4096, 11008, 4096
-    fx = (torch.randn(FM, FK, generator=g) / FK**0.5).to(torch.float16).to(dev)
-    fw = (torch.randn(FK, FN, generator=g) / FK**0.5).to(torch.float16).to(dev)
-    fb = (0.02 * torch.randn(FN, generator=g)).to(torch.float16).to(dev)
     fcfg, src = pick("fused_linear", "fp16", M=FM, N=FN, K=FK)
     assert_verified(linear_gelu_reference(fx, fw, fb), fused_linear_gelu(fx, fw, fb, config=fcfg),
                     context="fused linear config 4")
@@ -322,17 +380,17 @@ def main(argv: list[str] | None = None) -> int:
     fused = record("fused_linear_fp16_4096x11008x4096",
                    [lambda c=c: fused_linear_gelu(c[0], c[1], c[2], config=fcfg) for c in cp],
                    metrics.matmul_flops(FM, FN, FK), "TFLOP/s", f16_peak, src)
-    tu = _time_flushed(lambda: linear_gelu_reference(fx, fw, fb), steps, warmup, flush)
+    mine, tu = _time_interleaved(lambda: fused_linear_gelu(fx, fw, fb, config=fcfg),
+                                 lambda: linear_gelu_reference(fx, fw, fb), steps, warmup, flush)
     fused["unfused_torch_3op_us"] = float(np.mean(tu)) * 1e3
-    fused["speedup_vs_unfused"] = fused["unfused_torch_3op_us"] / fused["mean_us"]
+    fused["interleaved_us"] = float(np.mean(mine)) * 1e3
+    fused["speedup_vs_unfused"] = float(np.mean(tu)) / float(np.mean(mine))
     ms, _ = (float("nan"), 0.0) if args.no_sustained else _time_graph([lambda c=c: linear_gelu_reference(c[0], c[1], c[2]) for c in cp],
                         steps, warmup, flush)
     fused["unfused_torch_3op_sustained_us"] = ms * 1e3
     del fx, fw, cp
 
     # --- config 5a: decode GEMV bf16 1x11008x4096 ----------------------------------
-    vx = (torch.rand(1, 4096, generator=g) * 2 - 1).to(torch.bfloat16).to(dev)
-    vw = (torch.rand(4096, 11008, generator=g) * 2 - 1).to(torch.bfloat16).to(dev)
     vcfg, src = pick("matmul", "bf16", M=1, N=11008, K=4096)
     assert_verified(torch.matmul(vx.float(), vw.float()), matmul(vx, vw, config=vcfg),
                     dtype=torch.bfloat16, context="gemv config 5a")
@@ -341,8 +399,10 @@ def main(argv: list[str] | None = None) -> int:
     gemv = record("gemv_bf16_1x11008x4096",
                   [lambda c=c: matmul(c[0], c[1], config=vcfg) for c in cp],
                   work, "GB/s", hbm, src)
-    tv = _time_flushed(lambda: torch.matmul(vx, vw), steps, warmup, flush)
+    mine, tv = _time_interleaved(lambda: matmul(vx, vw, config=vcfg), lambda: torch.matmul(vx, vw),
+                                 steps, warmup, flush)
     gemv["torch_gbps"] = work / (np.mean(tv) * 1e-3) / 1e9
+    gemv["interleaved_us"] = float(np.mean(mine)) * 1e3
     ms, _ = (float("nan"), 0.0) if args.no_sustained else _time_graph([lambda c=c: torch.matmul(c[0], c[1]) for c in cp], steps, warmup, flush)
     gemv["torch_sustained_gbps"] = work / (ms * 1e-3) / 1e9
     del cp
@@ -350,9 +410,6 @@ def main(argv: list[str] | None = None) -> int:
     # --- widened rows: vector_add (the HBM probe) and the two-pass RMSNorm --------
     from kernelforge.kernels.vector_add import vector_add
 
-    VN = 1 << 26
-    va = torch.randn(VN, generator=g).to(dev)
-    vb = torch.randn(VN, generator=g).to(dev)
     acfg, src = pick("vector_add", "fp32", n=VN)
     assert torch.equal(vector_add(va, vb, config=acfg), va + vb), "vector_add must be bit-exact"
     work = metrics.vector_add_bytes(VN, 4)
@@ -360,13 +417,12 @@ def main(argv: list[str] | None = None) -> int:
     vadd = record("vector_add_fp32_67108864",
                   [lambda c=c: vector_add(c[0], c[1], config=acfg) for c in cp],
                   work, "GB/s", hbm, src)
-    ta = _time_flushed(lambda: va + vb, steps, warmup, flush)
+    mine, ta = _time_interleaved(lambda: vector_add(va, vb, config=acfg), lambda: va + vb, steps,
+                                 warmup, flush)
     vadd["torch_gbps"] = work / (np.mean(ta) * 1e-3) / 1e9
+    vadd["interleaved_us"] = float(np.mean(mine)) * 1e3
     del cp, va, vb
 
-    WR, WC = 4096, 32768
-    wx = torch.randn(WR, WC, generator=g).to(torch.float16).to(dev)
-    wg = (1.0 + 0.1 * torch.randn(WC, generator=g)).to(torch.float16).to(dev)
     wcfg, src = pick("rmsnorm", "fp16", rows=WR, cols=WC)
     assert_verified(rmsnorm_reference(wx, wg, eps=1e-6), rmsnorm(wx, wg, eps=1e-6, config=wcfg),
                     context="two-pass rmsnorm")
@@ -375,8 +431,10 @@ def main(argv: list[str] | None = None) -> int:
     wide = record(f"rmsnorm_two_pass_fp16_{WR}x{WC}",
                   [lambda c=c: rmsnorm(c[0], c[1], eps=1e-6, config=wcfg) for c in cp],
                   work, "GB/s", hbm, src)
-    tw = _time_flushed(lambda: rmsnorm_reference(wx, wg, eps=1e-6), steps, warmup, flush)
+    mine, tw = _time_interleaved(lambda: rmsnorm(wx, wg, eps=1e-6, config=wcfg),
+                                 lambda: rmsnorm_reference(wx, wg, eps=1e-6), steps, warmup, flush)
     wide["torch_eager_gbps"] = work / (np.mean(tw) * 1e-3) / 1e9
+    wide["interleaved_us"] = float(np.mean(mine)) * 1e3
     del cp
 
     # --- CPU baseline: the oracle on the host cores, bounded slices ----------------
