@@ -29,7 +29,9 @@ The torch comparators (hipBLASLt, the unfused matmul + bias + GELU, torch's
 GEMV, ``a + b``, eager RMSNorm) are timed the same way but alternating step by
 step with the kernel they are compared to (``interleaved_us`` is that
 kernel's mean in the same run), so a ratio of the two is not skewed by the
-clock rising or falling between two runs.
+clock rising or falling between two runs. Per configuration the order is:
+correctness gate, interleaved comparison, then the configuration's own W
+warm-up and K timed steps (the comparison's launches precede them).
 
 Each configuration's output is checked against torch on the same device with
 the reference's gate before it is timed. The CPU baseline is the oracle
@@ -359,12 +361,12 @@ def main(argv: list[str] | None = None) -> int:
     with exact_fp32_matmul():
         assert_verified(torch.matmul(a.float(), b.float()), matmul(a, b, config=gcfg),
                         dtype=torch.float16, context="gemm config 3")
+    mine, tg = _time_interleaved(lambda: matmul(a, b, config=gcfg), lambda: torch.matmul(a, b),
+                                 steps, warmup, flush)
     r, cp = copies_of((M * K + K * N + M * N) * 2, a, b)
     gemm = record("gemm_fp16_2048x4096x4096",
                   [lambda c=c: matmul(c[0], c[1], config=gcfg) for c in cp],
                   metrics.matmul_flops(M, N, K), "TFLOP/s", f16_peak, src)
-    mine, tg = _time_interleaved(lambda: matmul(a, b, config=gcfg), lambda: torch.matmul(a, b),
-                                 steps, warmup, flush)
     gemm["torch_hipblaslt_tflops"] = metrics.matmul_flops(M, N, K) / (np.mean(tg) * 1e-3) / 1e12
     gemm["interleaved_us"] = float(np.mean(mine)) * 1e3
     gemm["speedup_vs_hipblaslt"] = float(np.mean(tg)) / float(np.mean(mine))
@@ -376,12 +378,12 @@ def main(argv: list[str] | None = None) -> int:
     fcfg, src = pick("fused_linear", "fp16", M=FM, N=FN, K=FK)
     assert_verified(linear_gelu_reference(fx, fw, fb), fused_linear_gelu(fx, fw, fb, config=fcfg),
                     context="fused linear config 4")
+    mine, tu = _time_interleaved(lambda: fused_linear_gelu(fx, fw, fb, config=fcfg),
+                                 lambda: linear_gelu_reference(fx, fw, fb), steps, warmup, flush)
     r, cp = copies_of(metrics.fused_linear_bytes(FM, FN, FK, 2, fused=True), fx, fw, fb)
     fused = record("fused_linear_fp16_4096x11008x4096",
                    [lambda c=c: fused_linear_gelu(c[0], c[1], c[2], config=fcfg) for c in cp],
                    metrics.matmul_flops(FM, FN, FK), "TFLOP/s", f16_peak, src)
-    mine, tu = _time_interleaved(lambda: fused_linear_gelu(fx, fw, fb, config=fcfg),
-                                 lambda: linear_gelu_reference(fx, fw, fb), steps, warmup, flush)
     fused["unfused_torch_3op_us"] = float(np.mean(tu)) * 1e3
     fused["interleaved_us"] = float(np.mean(mine)) * 1e3
     fused["speedup_vs_unfused"] = float(np.mean(tu)) / float(np.mean(mine))
@@ -395,12 +397,12 @@ def main(argv: list[str] | None = None) -> int:
     assert_verified(torch.matmul(vx.float(), vw.float()), matmul(vx, vw, config=vcfg),
                     dtype=torch.bfloat16, context="gemv config 5a")
     work = metrics.matmul_bytes(1, 11008, 4096, 2)
+    mine, tv = _time_interleaved(lambda: matmul(vx, vw, config=vcfg), lambda: torch.matmul(vx, vw),
+                                 steps, warmup, flush)
     r, cp = copies_of(work, vx, vw)
     gemv = record("gemv_bf16_1x11008x4096",
                   [lambda c=c: matmul(c[0], c[1], config=vcfg) for c in cp],
                   work, "GB/s", hbm, src)
-    mine, tv = _time_interleaved(lambda: matmul(vx, vw, config=vcfg), lambda: torch.matmul(vx, vw),
-                                 steps, warmup, flush)
     gemv["torch_gbps"] = work / (np.mean(tv) * 1e-3) / 1e9
     gemv["interleaved_us"] = float(np.mean(mine)) * 1e3
     ms, _ = (float("nan"), 0.0) if args.no_sustained else _time_graph([lambda c=c: torch.matmul(c[0], c[1]) for c in cp], steps, warmup, flush)
@@ -413,12 +415,12 @@ def main(argv: list[str] | None = None) -> int:
     acfg, src = pick("vector_add", "fp32", n=VN)
     assert torch.equal(vector_add(va, vb, config=acfg), va + vb), "vector_add must be bit-exact"
     work = metrics.vector_add_bytes(VN, 4)
+    mine, ta = _time_interleaved(lambda: vector_add(va, vb, config=acfg), lambda: va + vb, steps,
+                                 warmup, flush)
     r, cp = copies_of(work, va, vb)
     vadd = record("vector_add_fp32_67108864",
                   [lambda c=c: vector_add(c[0], c[1], config=acfg) for c in cp],
                   work, "GB/s", hbm, src)
-    mine, ta = _time_interleaved(lambda: vector_add(va, vb, config=acfg), lambda: va + vb, steps,
-                                 warmup, flush)
     vadd["torch_gbps"] = work / (np.mean(ta) * 1e-3) / 1e9
     vadd["interleaved_us"] = float(np.mean(mine)) * 1e3
     del cp, va, vb
@@ -427,12 +429,12 @@ def main(argv: list[str] | None = None) -> int:
     assert_verified(rmsnorm_reference(wx, wg, eps=1e-6), rmsnorm(wx, wg, eps=1e-6, config=wcfg),
                     context="two-pass rmsnorm")
     work = metrics.rmsnorm_bytes(WR, WC, 2)
+    mine, tw = _time_interleaved(lambda: rmsnorm(wx, wg, eps=1e-6, config=wcfg),
+                                 lambda: rmsnorm_reference(wx, wg, eps=1e-6), steps, warmup, flush)
     r, cp = copies_of(work, wx, wg)
     wide = record(f"rmsnorm_two_pass_fp16_{WR}x{WC}",
                   [lambda c=c: rmsnorm(c[0], c[1], eps=1e-6, config=wcfg) for c in cp],
                   work, "GB/s", hbm, src)
-    mine, tw = _time_interleaved(lambda: rmsnorm(wx, wg, eps=1e-6, config=wcfg),
-                                 lambda: rmsnorm_reference(wx, wg, eps=1e-6), steps, warmup, flush)
     wide["torch_eager_gbps"] = work / (np.mean(tw) * 1e-3) / 1e9
     wide["interleaved_us"] = float(np.mean(mine)) * 1e3
     del cp
