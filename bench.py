@@ -23,7 +23,12 @@ and the K steps (step i uses copy i mod R and keeps its own output) are
 captured into one HIP graph whose replay is event-timed. That removes host
 launch cost but keeps the dependency drain between consecutive kernels and
 the clock the GPU holds under sustained load. Each replay's outputs are
-checked bitwise against the eager outputs.
+checked bitwise against the eager outputs. After every configuration, a soak
+replays the headline GEMM's graph back to back for ``--soak-seconds`` (8 by
+default) and reports its per-launch time as ``soak`` on that configuration:
+the GPU busy without a gap for seconds, at its sustained clock. The amdgpu
+driver's own busy percentage (sysfs ``gpu_busy_percent``) is sampled every
+0.1 s meanwhile and reported beside it.
 
 The torch comparators (hipBLASLt, the unfused matmul + bias + GELU, torch's
 GEMV, ``a + b``, eager RMSNorm) are timed the same way but alternating step by
@@ -151,6 +156,96 @@ def _time_graph(fns, steps: int, warmup: int, flush):
     return ms, dev
 
 
+def _soak(fns, seconds: float, steps: int) -> dict:
+    """Back-to-back replays of one graph of ``steps`` launches for about ``seconds``.
+
+    ``fns[i]`` runs the step on input copy i and returns its output, as in
+    ``_time_graph``. The GPU runs this one kernel without a gap for the whole
+    window, long enough for a utilisation sampler outside the process to see it
+    and for the board to reach its sustained power and clock. The host waits
+    for every batch of replays, so the queue stays short. After the window the
+    last replay's outputs are checked bitwise against eager runs of the same
+    copies.
+    """
+    import torch
+
+    n = len(fns)
+    eager = [fns[i]() for i in range(n)]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = [fns[j % n]() for j in range(steps)]
+    graph.replay()
+    torch.cuda.synchronize()
+    batch = max(1, 2000 // steps)  # about 2000 launches per host wait
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    replays = 0
+    t0 = time.perf_counter()
+    start.record()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(batch):
+            graph.replay()
+        replays += batch
+        torch.cuda.synchronize()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    for j in range(min(steps, n)):
+        if not torch.equal(outs[j], eager[j]):
+            raise RuntimeError(f"soak: replay output {j} differs from the eager result")
+    launches = replays * steps
+    ms = start.elapsed_time(end)
+    del graph, outs, eager
+    return {"launches": launches, "gpu_seconds": ms / 1e3, "wall_seconds": wall,
+            "us_per_launch": ms * 1e3 / launches}
+
+
+def _busy_path(dev) -> Path | None:
+    """The amdgpu driver's busy-percentage file of ``dev`` in sysfs, if readable."""
+    import torch
+
+    p = torch.cuda.get_device_properties(dev)
+    path = Path(f"/sys/bus/pci/devices/{p.pci_domain_id:04x}:{p.pci_bus_id:02x}:"
+                f"{p.pci_device_id:02x}.0/gpu_busy_percent")
+    try:
+        int(path.read_text().strip())
+    except (OSError, ValueError):
+        return None
+    return path
+
+
+class _BusySampler:
+    """Reads the GPU's busy percentage every ``period`` seconds on a thread."""
+
+    def __init__(self, path: Path, period: float = 0.1):
+        import threading
+
+        self.path, self.period = path, period
+        self.samples: list[int] = []
+        self._stop = threading.Event()
+        self._thread = threading.Thread(target=self._run, daemon=True)
+
+    def _run(self) -> None:
+        while not self._stop.wait(self.period):
+            try:
+                self.samples.append(int(self.path.read_text().strip()))
+            except (OSError, ValueError):
+                pass
+
+    def __enter__(self):
+        self._thread.start()
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self._stop.set()
+        self._thread.join()
+
+    def summary(self) -> dict:
+        n = len(self.samples)
+        return {"source": str(self.path), "period_s": self.period, "samples": n,
+                "mean_pct": sum(self.samples) / n if n else None,
+                "min_pct": min(self.samples) if n else None}
+
+
 def _cpu_time(fn, seconds: float) -> tuple[float, int]:
     """Mean seconds per call over at least ``seconds`` of calls (after one warm call)."""
     fn()  # warm caches / thread pool
@@ -199,7 +294,11 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-sustained", action="store_true",
-                        help="skip the graph-captured sustained runs (profiling the headline method)")
+                        help="skip the graph-captured sustained runs and the soak (profiling the "
+                             "headline method)")
+    parser.add_argument("--soak-seconds", type=float, default=8.0,
+                        help="seconds of back-to-back headline GEMM launches after the configs "
+                             "(0 skips)")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(
@@ -438,6 +537,26 @@ def main(argv: list[str] | None = None) -> int:
     wide["torch_eager_gbps"] = work / (np.mean(tw) * 1e-3) / 1e9
     wide["interleaved_us"] = float(np.mean(mine)) * 1e3
     del cp
+
+    # --- soak: the headline GEMM back to back for a few seconds --------------------
+    if not args.no_sustained and args.soak_seconds > 0:
+        _log(f"soak: gemm_fp16_2048x4096x4096 back to back for {args.soak_seconds:.0f} s")
+        r, cp = copies_of((M * K + K * N + M * N) * 2, a, b)
+        fns = [lambda c=c: matmul(c[0], c[1], config=gcfg) for c in cp]
+        path = _busy_path(dev)
+        if path is None:
+            soak = _soak(fns, args.soak_seconds, steps)
+            soak["gpu_busy"] = None
+        else:
+            with _BusySampler(path) as sampler:
+                soak = _soak(fns, args.soak_seconds, steps)
+            soak["gpu_busy"] = sampler.summary()
+        soak["value"] = metrics.matmul_flops(M, N, K) / (soak["us_per_launch"] * 1e-6) / 1e12
+        soak["unit"] = "TFLOP/s"
+        gemm["soak"] = soak
+        _log(f"soak: {soak['launches']} launches, {soak['us_per_launch']:.1f} us each = "
+             f"{soak['value']:.1f} TFLOP/s")
+        del cp
 
     # --- CPU baseline: the oracle on the host cores, bounded slices ----------------
     # About 4 s of calls per workload (about 20 s in all), on bounded slices of the
