@@ -7,7 +7,8 @@ kernelforge/tests/test_fused_linear.py:176-204, through
 kernelforge/profiling/pytorch_profiler.py:91-135).
 
 The same count pins every entry point to a single launch per call at the
-configurations bench.py times. The split-K GEMM and the split-K GEMV finish
+configurations bench.py times, and at the fused shape on a split-K tile. The
+split-K GEMM and the split-K GEMV finish
 their cross-program reduction inside that launch, and their counters are
 reset by the kernel itself, so once a workspace exists no fill or memset
 kernel runs ahead of a call.
@@ -78,11 +79,15 @@ def _timed_cases():
         b = torch.randn(4096, 4096, device=DEV).div_(64).half()
         return lambda: matmul(a, b, config=cfg)
 
-    def fused():
+    def fused(split: bool):
         from kernelforge.kernels.fused_linear import fused_linear_gelu
+        from kernelforge.tuning.config import KernelConfig
 
-        cfg = _packaged("fused_linear", "fp16", M=4096, N=11008, K=4096)
-        assert cfg.get("SPLIT_K", 1) > 1, dict(cfg)  # the split-K tail runs in this launch
+        if split:  # the 256x128 tile, last round split in two: the tail runs in this launch
+            cfg = KernelConfig("fused_linear", BLOCK_M=256, BLOCK_N=128, BLOCK_K=64, DIRECT=1,
+                               GROUP_M=4, SPLIT_K=2, num_stages=3, num_warps=8)
+        else:
+            cfg = _packaged("fused_linear", "fp16", M=4096, N=11008, K=4096)
         x = torch.randn(4096, 4096, device=DEV).div_(64).half()
         w = torch.randn(4096, 11008, device=DEV).div_(64).half()
         bias = torch.randn(11008, device=DEV).mul_(0.02).half()
@@ -120,7 +125,9 @@ def _timed_cases():
         b = torch.randn(1 << 26, device=DEV)
         return lambda: run(a, b, config=cfg)
 
-    return [("gemm_fp16_2048x4096x4096", gemm), ("fused_linear_fp16_4096x11008x4096", fused),
+    return [("gemm_fp16_2048x4096x4096", gemm),
+            ("fused_linear_fp16_4096x11008x4096", lambda: fused(False)),
+            ("fused_linear_fp16_4096x11008x4096_split_k", lambda: fused(True)),
             ("gemv_bf16_1x11008x4096", gemv), ("softmax_fp16_8192x4096", softmax),
             ("rmsnorm_fp32_4096x4096", rmsnorm), ("vector_add_fp32_67108864", vector_add)]
 
