@@ -137,11 +137,13 @@ def _time_graph(fns, steps: int, warmup: int, flush):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         outs = [fns[j % n]() for j in range(steps)]  # every output stays live
-    graph.replay()  # untimed replay
     torch.cuda.synchronize()
-    flush.flush()
-    torch.cuda.synchronize()
+    # The untimed replay, the flush and the timed replay are queued back to back:
+    # a host wait between them would leave the GPU idle, and MFMA-heavy launches
+    # after an idle period run at a lower clock for their first milliseconds.
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    graph.replay()  # untimed replay
+    flush.flush()
     start.record()
     graph.replay()
     end.record()
