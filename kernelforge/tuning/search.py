@@ -530,11 +530,16 @@ class _GemmSpace(SearchSpace):
         latency), else 4, and fewer for register-staged tiles (more registers
         each); (6) the taller of two
         transposed tiles; (7) least padding waste.
-        GEMV: HBM-bound, so (1) at least one workgroup per CU, (2) at least
-        four waves per CU (each keeps 16 x 16 bytes per lane in flight, and
-        HBM needs ~32 KiB in flight per CU), then fewer slices (a shorter
-        cross-slice tail), 16-lane row segments, and fewer waves. GEMV
-        candidates sort ahead of MFMA tiles for decode shapes.
+        GEMV strips: HBM-bound, so (1) one round of workgroups (a second
+        round doubles some CUs' streams), (2) as many workgroups as that
+        round allows, (3) strips of at least 512 bytes per row (narrower
+        pieces share 128-byte lines between workgroups, whose CUs then fetch
+        them twice), (4) eight waves (the most bytes in flight per CU), (5)
+        fewer slices (a shorter cross-slice tail). Measured at 1x11008x4096
+        bf16 (kernel-only): 172 workgroups of 512-byte strips stream at 97%
+        of 256 workgroups' rate, while 256-byte and 128-byte strips and grids
+        past one round are slower. GEMV candidates sort ahead of MFMA tiles
+        for decode shapes.
         """
         dims = problem.dims_dict
         programs = self.num_programs(config, problem)
@@ -546,15 +551,14 @@ class _GemmSpace(SearchSpace):
             return (0, -min(programs, caps.cu_count), config["SPLIT_K"], -lanes,
                     abs(config["num_warps"] - 4))
         if config.get("GEMV"):
-            waves = programs * config["num_warps"]
             lanes = config.get("LANES_PER_ROW", GEMV_DEFAULT_LANES_PER_ROW)
             return (
                 0,
+                programs > caps.cu_count,
                 -min(programs, caps.cu_count),
-                -min(waves, 4 * caps.cu_count),
+                -min(lanes * VECTOR_BYTES, 512),
+                abs(config["num_warps"] - 8),
                 config["SPLIT_K"],
-                abs(lanes.bit_length() - 5),  # 16 lanes per row measured best
-                config["num_warps"],
             )
         bm, bn = config["BLOCK_M"], config["BLOCK_N"]
         direct = config.get("DIRECT", 0)

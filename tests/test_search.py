@@ -201,6 +201,29 @@ def test_gemv_rules():
     assert space.reject_reason(narrow, _gemm(8, 4096, 4096, "bf16"), MI355X_CAPS) is None
 
 
+def _packaged_gemv_strip_winners():
+    import json
+    from pathlib import Path
+
+    path = Path(__file__).resolve().parents[1] / "kernelforge" / "tuned" / "mi355x_gfx950.json"
+    entries = json.loads(path.read_text())["entries"]["AMD_Instinct_MI355X_gfx950"]
+    return [(op, dt, shape, entry["config"])
+            for op, by_dtype in entries.items() for dt, by_shape in by_dtype.items()
+            for shape, entry in by_shape.items()
+            if entry["config"].get("GEMV") and not shape.endswith("+bt")]
+
+
+@pytest.mark.parametrize("op,dt,shape,cfg", _packaged_gemv_strip_winners(),
+                         ids=lambda v: v if isinstance(v, str) else "")
+def test_packaged_gemv_winners_are_within_the_default_budget(op, dt, shape, cfg):
+    """A default `tune` of a decode shape measures the configuration that a wider
+    sweep found best: the strip priority (one round, full fill, 512-byte strips,
+    eight waves, fewer slices) ranks each packaged winner inside the budget."""
+    m, n, k = map(int, shape.split("x"))
+    cands = search_space(op).candidates(Problem.create(op, dt, M=m, N=n, K=k), MI355X_CAPS)
+    assert KernelConfig(op, **cfg) in cands, (shape, cfg, len(cands))
+
+
 def test_gemv_strip_width_sets_the_workgroup_count():
     space = MatmulSearchSpace()
     problem = _gemm(1, 11008, 4096, "bf16")
