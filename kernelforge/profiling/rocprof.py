@@ -179,6 +179,19 @@ def measured_dispatch(dispatches: list[Dispatch]) -> Dispatch | None:
     return ours[-1] if ours else None
 
 
+def allocated_vgprs(vgpr_count: int) -> int:
+    """Vector registers a gfx950 wave is given, from rocprofv3's ``VGPR_Count``.
+
+    The kernel descriptor holds the allocation as a count of 8-register
+    granules; rocprofv3 multiplies that count by 4, so on gfx950 its field
+    reads half the allocation. Checked against the ``.vgpr_count`` of this
+    library's own code objects: 223 and 256 registers (the 128x256 and
+    256x256 GEMM tiles) read 112 and 128, 56 and 79 (softmax and RMSNorm
+    rows) read 28 and 40.
+    """
+    return 2 * vgpr_count
+
+
 @dataclass
 class LaunchCounters:
     """Counters and derived figures of one launch, merged over the passes."""
@@ -248,7 +261,9 @@ class RocprofRun:
             return "\n".join(lines)
         c = self.launch
         rows = [("kernel", c.kernel[:100]), ("grid / workgroup", f"{c.grid} / {c.workgroup} lanes"),
-                ("VGPR / AGPR / scratch", f"{c.vgprs} / {c.agprs} / {c.scratch_bytes} B"),
+                ("VGPR / AGPR / scratch",
+                 f"{allocated_vgprs(c.vgprs)} / {c.agprs} / {c.scratch_bytes} B "
+                 f"(VGPR_Count {c.vgprs} x 2)"),
                 ("LDS", f"{c.lds_bytes} B")]
         if c.duration_us:
             rows.append(("duration", f"{c.duration_us:.1f} us"))

@@ -107,6 +107,17 @@ def test_trace_csv_supplies_duration_and_launch_shape(tmp_path):
     assert launch.shader_clock_ghz(256) == pytest.approx(1.862, abs=2e-3)
 
 
+def test_vgpr_field_reads_half_the_gfx950_allocation():
+    # .vgpr_count of this library's code objects against the VGPR_Count that
+    # rocprofv3 recorded for the same kernels on an MI355X: (allocated, field).
+    for allocated, field in ((223, 112), (256, 128), (56, 28), (79, 40)):
+        assert rocprof.allocated_vgprs(field) == -(-allocated // 8) * 8
+    launch = rocprof.LaunchCounters(kernel=GEMM, grid=131072, workgroup=512, vgprs=112)
+    text = rocprof.RocprofRun([["rocprofv3"]], [0], launch).render(
+        flops=1, algorithmic_bytes=1, peak_tflops=1, peak_gbps=1, cu_count=256, memory_bound=False)
+    assert "224 / 0 / 0 B (VGPR_Count 112 x 2)" in text
+
+
 def test_hbm_bytes_use_the_copy_calibration():
     launch = rocprof.LaunchCounters(counters={"FETCH_SIZE": 1024.0, "WRITE_SIZE": 2048.0})
     assert launch.hbm_bytes == (2.0 * 1024 + 1.0 * 2048) * 1024
