@@ -598,11 +598,13 @@ def _profile_rocprof(session: _Session) -> int:
         result = rocprof.run(target, out_dir=out_dir, passes=tuple(args.passes))
     print(_problem_banner(problem))
     flops, moved = operator.flops(problem), operator.bytes_moved(problem)
+    # fp32 products run on the fp32 MFMAs, a sixteenth of the 16-bit rate.
+    peak = MI355X_CAPS.peak_fp32_tflops if problem.itemsize == 4 else MI355X_CAPS.peak_fp16_tflops
     # A product below the ridge point (peak FLOP/s over peak bytes/s, about
     # 315 FLOP/byte for 16-bit MFMA) is bandwidth-bound, e.g. a decode GEMV.
-    ridge = MI355X_CAPS.peak_fp16_tflops * 1e3 / MI355X_CAPS.peak_hbm_gbps
+    ridge = peak * 1e3 / MI355X_CAPS.peak_hbm_gbps
     bound_by_hbm = operator.is_memory_bound() or flops < ridge * moved
-    print(result.render(flops=flops, algorithmic_bytes=moved, peak_tflops=MI355X_CAPS.peak_fp16_tflops,
+    print(result.render(flops=flops, algorithmic_bytes=moved, peak_tflops=peak,
                         peak_gbps=MI355X_CAPS.peak_hbm_gbps, cu_count=MI355X_CAPS.cu_count,
                         memory_bound=bound_by_hbm))
     return 0 if result.ok else 1

@@ -169,3 +169,17 @@ def test_nsight_backend_reports_unavailable(capsys):
 
     assert main(["profile", "matmul", "--backend", "nsight"]) == 2
     assert "ncu not found" in capsys.readouterr().err
+
+
+@pytest.mark.parametrize("dtype,peak", (("fp32", "157.3"), ("fp16", "2516.6")))
+def test_profile_prices_each_dtype_against_its_own_mfma_peak(monkeypatch, capsys, dtype, peak):
+    from kernelforge.cli.main import main
+
+    launch = rocprof.LaunchCounters(kernel=GEMM, grid=131072, workgroup=512, duration_us=500.0)
+    monkeypatch.setattr(rocprof, "rocprof_available", lambda: True)
+    monkeypatch.setattr(rocprof, "run", lambda *a, **k: rocprof.RocprofRun([["rocprofv3"]], [0], launch))
+    assert main(["profile", "matmul", "-m", "2048", "-n", "4096", "-k", "4096", "--dtype", dtype,
+                 "--backend", "rocprof", "--no-cache"]) == 0
+    # 68,719,476,736 FLOP in 500 us = 137.4 TFLOP/s.
+    tflops = 68_719_476_736 / 500e-6 / 1e12
+    assert f"{tflops:.1f} TFLOP/s = {100 * tflops / float(peak):.1f}% of peak" in capsys.readouterr().out
