@@ -189,8 +189,13 @@ class SearchSpace(ABC):
         survivors = [c for c in feasible if c not in dropped]
         ranked = sorted(survivors, key=lambda c: (*self.priority(c, problem, machine), c.to_json()))
         return CandidateSet(problem=problem, generated=len(points), feasible=len(feasible),
-                            after_prune=len(ranked), budget=budget, candidates=ranked[:budget],
+                            after_prune=len(ranked), budget=budget,
+                            candidates=self.select(ranked, budget, problem),
                             rejected=tuple(rejected))
+
+    def select(self, ranked: list[KernelConfig], budget: int, problem: Problem) -> list[KernelConfig]:
+        """The candidates the budget measures, from the ranked survivors."""
+        return ranked[:budget]
 
     def explain(self, problem: Problem, caps: DeviceCaps | None = None) -> str:
         """The stage counts and rejections by rule, for ``tune --explain``."""
@@ -414,6 +419,21 @@ class _GemmSpace(SearchSpace):
                 yield KernelConfig(
                     self.operation, GEMV=1, SPLIT_K=split, LANES_PER_ROW=lanes, num_warps=warps
                 )
+
+    #: Decode batches of at least this many rows keep a third of the budget for
+    #: MFMA tiles, which rank behind every GEMV candidate: at 8 rows a split
+    #: 32-row tile can beat the strip kernel, whose per-lane accumulators grow
+    #: with the rows.
+    GEMV_SHARED_BUDGET_M = 4
+
+    def select(self, ranked: list[KernelConfig], budget: int, problem: Problem) -> list[KernelConfig]:
+        m = problem.dims_dict["M"]
+        if not self.GEMV_SHARED_BUDGET_M <= m <= self.GEMV_MAX_M:
+            return ranked[:budget]
+        gemv = [c for c in ranked if c.get("GEMV")]
+        tiles = [c for c in ranked if not c.get("GEMV")]
+        keep = gemv[: budget - min(len(tiles), budget // 3)]
+        return keep + tiles[: budget - len(keep)]
 
     def num_programs(self, config: KernelConfig, problem: Problem) -> int:
         dims = problem.dims_dict
