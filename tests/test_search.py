@@ -453,3 +453,13 @@ def test_explain_names_the_device_and_every_stage():
     assert "MI355X" in text and "256 CUs" in text and "160 KiB LDS" in text
     for stage in ("grid points", "feasible", "after prune", "selected (budget)"):
         assert stage in text
+
+
+@pytest.mark.parametrize("m,tiles", [(1, 0), (2, 0), (4, 16), (8, 16)])
+def test_decode_batches_of_four_rows_or_more_measure_tiles_too(m, tiles):
+    cands = MatmulSearchSpace().candidates(_gemm(m, 11008, 4096, "bf16"), MI355X_CAPS)
+    assert len(cands) == DEFAULT_MAX_CANDIDATES
+    assert sum(1 for c in cands if not c.get("GEMV")) == tiles
+    first_tile = next((i for i, c in enumerate(cands) if not c.get("GEMV")), len(cands))
+    assert all(c.get("GEMV") for c in cands[:first_tile])
+    assert not any(c.get("GEMV") for c in cands[first_tile:])
