@@ -155,7 +155,7 @@ def _environment(db: ResultsDB) -> list[str]:
     latest = runs[-1]
     fields = (("GPU", "gpu_name"), ("Architecture", "gpu_arch"), ("Compute units", "cu_count"),
               ("HIP", "hip_version"), ("Driver", "driver_version"), ("PyTorch", "torch_version"),
-              ("kernelforge", "package_version"), ("Recorded", "timestamp"))
+              ("kernelforge", "kernelforge_version"), ("Recorded", "timestamp"))
     return ["| Field | Value |", "| --- | --- |"] + [
         f"| {title} | {latest.get(key) or '-'} |" for title, key in fields]
 

@@ -578,6 +578,9 @@ def _launch_once(session: _Session) -> int:
     flush_buffer(device).flush()
     operator.run(config, *inputs)
     torch.cuda.synchronize(device)
+    from kernelforge.profiling.rocprof import CHILD_DONE
+
+    print(CHILD_DONE, flush=True)  # the parent tells a finished child from one that died
     return 0
 
 

@@ -309,6 +309,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   int dtid = tid;
   if constexpr (Tl::MF == 32) asm volatile("" : "+v"(dtid));
   constexpr int kRowsPerIter = NT / 8;  // k-contiguous rows (A, BLAYOUT 1) per DMA instruction
+  // Chunk j of a lane reuses the k swizzle of its row kr for row kr + j*kRowsPerIter;
+  // swz_k reads row bits 1..3, so the row step must be a multiple of 16.
+  static_assert(kRowsPerIter % 16 == 0, "the DMA row step (lanes / 8) must keep the k swizzle: two or more waves");
   const int kr = dtid >> 3;             // this lane's row within an instruction's rows
   const int kc = swz_k(dtid & 7, kr) * 8;  // its k within the slice; same for every j
   uint32_t a_off[Tl::kAIters];

@@ -716,8 +716,10 @@ extern "C" int kf_gemv_no_alloc(int dtype, const void* x, const void* W, const v
   if (!needs_scratch)
     return gemv_entry(dtype, x, W, bias, y, M, N, K, ldx_m, ldx_k, ldw_k, ldw_n, ldy_m, ldy_n,
                       epilogue, split_k, waves, lanes_per_row, nullptr, 0, stream);
+  // Only the size is checked here; shapes kf_gemv refuses for other reasons
+  // (more column blocks than counters) get its own error from gemv_entry.
   const size_t need = kf_gemv_workspace_bytes(M, N, split_k);
-  if (need > static_cast<size_t>(KF_GEMV_NO_ALLOC_SCRATCH_BYTES) || N > KF_WORKSPACE_COUNTERS) {
+  if (need > static_cast<size_t>(KF_GEMV_NO_ALLOC_SCRATCH_BYTES)) {
     set_error("gemv_no_alloc: split_k=%d over %lldx%lld outputs needs %zu bytes of workspace, "
               "more than the %d bytes of static scratch; use kf_gemv with a workspace",
               split_k, (long long)M, (long long)N, need, KF_GEMV_NO_ALLOC_SCRATCH_BYTES);

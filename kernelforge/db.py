@@ -3,10 +3,13 @@
 Every result row points at the run that produced it (host, GPU, HIP, torch and
 package versions), the problem, and the configuration, so a number from last
 week stays comparable -- or visibly not -- with one from today. The tables are
-the reference's (kernelforge/db.py:35-99) so existing report queries keep
-working; the vendor-specific provenance columns name what this build records
-(``hip_version`` and ``cu_count`` in place of CUDA/Triton versions and an SM
-count).
+the reference's (kernelforge/db.py:35-99), every column included, so a file
+either tool created is read and written by the other: this build leaves
+``triton_version`` and ``cuda_version`` empty, stores its compute-unit count in
+``sm_count`` as well, and records what only it knows in two extra columns,
+``hip_version`` and ``cu_count``. Opening a file the reference created adds
+those two (nullable) columns; the reference names its columns in every
+statement, so it keeps working on the widened table.
 
 Here the schema is data: each table is a tuple of column declarations from
 which the DDL and every INSERT are generated, so a column cannot be added to
@@ -48,15 +51,19 @@ _TABLES: dict[str, tuple[_Columns, tuple[str, ...]]] = {
             ("platform", "TEXT"),
             ("python_version", "TEXT"),
             ("torch_version", "TEXT"),
-            ("hip_version", "TEXT"),
+            ("triton_version", "TEXT"),
+            ("cuda_version", "TEXT"),
             ("driver_version", "TEXT"),
             ("gpu_name", "TEXT"),
             ("gpu_arch", "TEXT"),
             ("gpu_memory_bytes", "INTEGER"),
-            ("cu_count", "INTEGER"),
+            ("sm_count", "INTEGER"),
             ("device_key", "TEXT NOT NULL"),
-            ("package_version", "TEXT"),
+            ("kernelforge_version", "TEXT"),
             ("notes", "TEXT NOT NULL DEFAULT ''"),
+            # This build's own provenance, after the reference's columns.
+            ("hip_version", "TEXT"),
+            ("cu_count", "INTEGER"),
         ),
         (),
     ),
@@ -135,7 +142,7 @@ _JOINED = {
     "p": ("operation", "shape_key", "dtype", "dims_json"),
     "c": ("params_json", "digest"),
     "run": ("run_id", "timestamp", "gpu_name", "gpu_arch", "device_key", "torch_version",
-            "hip_version", "driver_version"),
+            "triton_version", "cuda_version", "driver_version", "hip_version"),
 }
 _FROM = ("FROM results AS r JOIN problems AS p ON p.problem_id = r.problem_id "
          "JOIN runs AS run ON run.run_id = r.run_id "
@@ -199,7 +206,22 @@ class ResultsDB:
             )
         with self._conn:
             self._conn.executescript(_ddl())
+            self._widen()
             self._conn.execute(f"PRAGMA user_version = {SCHEMA_VERSION}")
+
+    def _widen(self) -> None:
+        """Add the columns of this build's schema an existing table lacks (a file
+        the reference created has no ``hip_version`` or ``cu_count``). Only
+        nullable columns can be missing; anything else is a foreign schema."""
+        for table, (columns, _) in _TABLES.items():
+            have = {row[1] for row in self._conn.execute(f"PRAGMA table_info({table})")}
+            for name, decl in columns:
+                if name in have:
+                    continue
+                if "NOT NULL" in decl or "PRIMARY KEY" in decl:
+                    raise RuntimeError(f"{self.path}: table {table} has no column {name}; "
+                                       "not a kernelforge results database")
+                self._conn.execute(f"ALTER TABLE {table} ADD COLUMN {name} {decl}")
 
     def __enter__(self) -> ResultsDB:
         return self
@@ -238,7 +260,10 @@ class ResultsDB:
     def start_run(self, env: Environment, *, notes: str = "", version: str = "") -> int:
         """Record the environment of a run; its id tags every result of that run."""
         values = {k: v for k, v in asdict(env).items() if k in _insertable("runs")}
-        values.update(package_version=version, notes=notes)
+        # No Triton and no CUDA here; the reference's SM-count column gets the
+        # compute-unit count, its nearest counterpart.
+        values.update(triton_version=None, cuda_version=None, sm_count=env.cu_count,
+                      kernelforge_version=version, notes=notes)
         with self._transaction():
             return self._insert("runs", values)
 

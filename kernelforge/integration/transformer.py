@@ -36,8 +36,9 @@ from kernelforge.tuning.cache import ConfigCache
 from kernelforge.tuning.config import KernelConfig, Problem
 
 BACKEND_TORCH = "torch"
-BACKEND_KERNELO = "kernelforge"
-BACKENDS = (BACKEND_TORCH, BACKEND_KERNELO)
+BACKEND_KERNELFORGE = "kernelforge"
+BACKEND_KERNELO = BACKEND_KERNELFORGE  # earlier name, kept for existing callers
+BACKENDS = (BACKEND_TORCH, BACKEND_KERNELFORGE)
 
 
 @dataclass(frozen=True)
@@ -121,7 +122,7 @@ class TransformerBlock(nn.Module):
     ) -> None:
         super().__init__()
         self.config = config or BlockConfig()
-        self._paths = {BACKEND_TORCH: _TorchPath(), BACKEND_KERNELO: _KernelPath(cache)}
+        self._paths = {BACKEND_TORCH: _TorchPath(), BACKEND_KERNELFORGE: _KernelPath(cache)}
         self.backend = backend
         h, inter = self.config.hidden, self.config.intermediate
         opts = {"device": device, "dtype": dtype}

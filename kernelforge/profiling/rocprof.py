@@ -66,6 +66,14 @@ SIMDS_PER_CU = 4
 #: MFMA "MOPS" count 512 FLOPs each (one 16x16x32 16-bit MFMA is 16384 FLOPs, 32 MOPS).
 FLOPS_PER_MOP = 512
 
+#: The last line the launch-once child prints once its measured launch has
+#: completed (cli/main.py); a pass whose log lacks it did not finish the program.
+CHILD_DONE = "kernelforge launch-once: done"
+
+#: Exit statuses of a process ended by SIGSEGV: as Popen reports it, and as a
+#: shell would.
+_SEGV = (-signal.SIGSEGV, 128 + signal.SIGSEGV)
+
 #: Kernels of this library live in namespace ``kf``; the profiler reports
 #: some names demangled (``void kf::...``) and others mangled (``_ZN2kf...``).
 LIBRARY_KERNEL_MARKS = ("kf::", "_ZN2kf")
@@ -242,10 +250,21 @@ class LaunchCounters:
 
 @dataclass
 class RocprofRun:
+    """The passes of one profile: their commands, status codes and the merged launch.
+
+    ``returncodes`` are the passes' verdicts; ``raw_returncodes`` what each
+    rocprofv3 process actually returned. The two differ only where rocprofv3
+    itself ended on SIGSEGV after the profiled program had printed its
+    completion line and the pass's output held the measured launch: that pass
+    is usable, and ``notes`` says what happened so that ``render`` prints it.
+    """
+
     commands: list[list[str]]
     returncodes: list[int]
     launch: LaunchCounters | None
     log: str = ""
+    raw_returncodes: list[int] = field(default_factory=list)
+    notes: list[str] = field(default_factory=list)
 
     @property
     def ok(self) -> bool:
@@ -254,6 +273,7 @@ class RocprofRun:
     def render(self, *, flops: int, algorithmic_bytes: int, peak_tflops: float,
                peak_gbps: float, cu_count: int, memory_bound: bool) -> str:
         lines = [f"$ {' '.join(c)}" for c in self.commands]
+        lines += [f"note: {n}" for n in self.notes]
         if self.launch is None:
             lines.append("no dispatch of a library kernel was recorded")
             if self.log.strip():
@@ -314,7 +334,7 @@ def run(target: list[str], *, out_dir: str | Path, passes: tuple[str, ...] = DEF
     if unknown:
         raise ValueError(f"unknown counter passes {unknown}; available: {sorted(PASSES)}")
     root = Path(out_dir)
-    commands, codes, logs = [], [], []
+    commands, codes, raw, logs, notes = [], [], [], [], []
     launch = LaunchCounters()
     found = False
     for name in passes:
@@ -327,14 +347,28 @@ def run(target: list[str], *, out_dir: str | Path, passes: tuple[str, ...] = DEF
         files = sorted(pass_dir.rglob(pattern))
         parse = parse_counter_csv if PASSES[name] else parse_trace_csv
         measured = measured_dispatch(parse(files[-1])) if files else None
-        # rocprofv3 itself may exit on a signal after the program has finished
-        # and its output is complete; such a pass counts as good.
-        codes.append(0 if measured is not None and rc in (-signal.SIGSEGV, 128 + signal.SIGSEGV)
-                     else rc)
+        raw.append(rc)
+        # rocprofv3 can end on SIGSEGV in its own teardown, after the program it
+        # ran has exited and its output files are written. Such a pass is used,
+        # and reported, only if the program got to its last line and the
+        # measured launch is in the output; any other signal or exit status
+        # fails the profile.
+        finished = CHILD_DONE in log
+        if rc in _SEGV and measured is not None and finished:
+            codes.append(0)
+            notes.append(f"pass '{name}': rocprofv3 exited on SIGSEGV (status {rc}) after the "
+                         "profiled program printed its completion line; the pass's output holds "
+                         "the measured launch and is used")
+        else:
+            codes.append(rc)
+            if rc in _SEGV:
+                notes.append(f"pass '{name}': rocprofv3 exited on SIGSEGV (status {rc}) "
+                             + ("before the profiled program finished" if not finished
+                                else "with no measured launch in its output"))
         if measured is None:
             if rc == 0:
                 codes[-1] = 1  # ran, but recorded no launch of this library
             break  # a failed pass ends the profile: nothing further runs on the GPU
         launch.absorb(measured, timed=not PASSES[name])
         found = True
-    return RocprofRun(commands, codes, launch if found else None, "\n".join(logs))
+    return RocprofRun(commands, codes, launch if found else None, "\n".join(logs), raw, notes)

@@ -36,6 +36,7 @@ KF_EPILOGUE_BIAS_GELU = 1
 KF_PIPELINE_STAGED = 0
 KF_PIPELINE_DIRECT = 1
 
+KF_WORKSPACE_COUNTERS = 1 << 18
 KF_WORKSPACE_COUNTER_BYTES = 4 << 18
 KF_GEMV_NO_ALLOC_SCRATCH_BYTES = 16 << 20
 

@@ -75,6 +75,85 @@ def test_db_schema_version_is_checked(tmp_path):
         ResultsDB(path)
 
 
+#: The reference's table layout (kernelforge/db.py:35-99 there): the column
+#: names and types a database it creates has. A file-format fixture, written
+#: out here so this test can build such a file without the reference.
+_REFERENCE_TABLES = {
+    "runs": "run_id INTEGER PRIMARY KEY AUTOINCREMENT, timestamp TEXT NOT NULL, hostname TEXT, "
+            "platform TEXT, python_version TEXT, torch_version TEXT, triton_version TEXT, "
+            "cuda_version TEXT, driver_version TEXT, gpu_name TEXT, gpu_arch TEXT, "
+            "gpu_memory_bytes INTEGER, sm_count INTEGER, device_key TEXT NOT NULL, "
+            "kernelforge_version TEXT, notes TEXT NOT NULL DEFAULT ''",
+    "problems": "problem_id INTEGER PRIMARY KEY AUTOINCREMENT, operation TEXT NOT NULL, "
+                "shape_key TEXT NOT NULL, dtype TEXT NOT NULL, dims_json TEXT NOT NULL, "
+                "UNIQUE (operation, shape_key, dtype)",
+    "configs": "config_id INTEGER PRIMARY KEY AUTOINCREMENT, operation TEXT NOT NULL, "
+               "digest TEXT NOT NULL, params_json TEXT NOT NULL, UNIQUE (operation, digest)",
+    "results": "result_id INTEGER PRIMARY KEY AUTOINCREMENT, run_id INTEGER NOT NULL, "
+               "problem_id INTEGER NOT NULL, config_id INTEGER, label TEXT NOT NULL, "
+               "status TEXT NOT NULL, correct INTEGER, rel_error REAL, median_us REAL, "
+               "mean_us REAL, std_us REAL, min_us REAL, max_us REAL, p95_us REAL, p99_us REAL, "
+               "warmup INTEGER, iterations INTEGER, timer TEXT, flushed_l2 INTEGER, tflops REAL, "
+               "gbps REAL, error TEXT NOT NULL DEFAULT ''",
+}
+
+#: How the reference records a run and reads results back (its column lists).
+_REFERENCE_RUN_INSERT = (
+    "INSERT INTO runs (timestamp, hostname, platform, python_version, torch_version, "
+    "triton_version, cuda_version, driver_version, gpu_name, gpu_arch, gpu_memory_bytes, "
+    "sm_count, device_key, kernelforge_version, notes) VALUES "
+    "('t', 'h', 'p', '3.10', '2.4', '3.0', '12.4', '550', 'A100', 'sm_80', 1, 108, "
+    "'NVIDIA_A100', '0.1', '')")
+_REFERENCE_ROWS_SELECT = (
+    "SELECT r.label, r.median_us, p.operation, c.digest, run.gpu_name, run.torch_version, "
+    "run.triton_version, run.cuda_version, run.driver_version, run.sm_count, "
+    "run.kernelforge_version FROM results AS r JOIN problems AS p ON p.problem_id = r.problem_id "
+    "JOIN runs AS run ON run.run_id = r.run_id LEFT JOIN configs AS c ON c.config_id = r.config_id")
+
+
+def test_db_opens_and_writes_a_file_the_reference_created(tmp_path):
+    """A database created with the reference's tables is widened (two nullable
+    columns) and recorded into; the reference's own statements keep working on
+    it and on a file this build created."""
+    import sqlite3
+
+    path = tmp_path / "reference.db"
+    con = sqlite3.connect(path)
+    for table, body in _REFERENCE_TABLES.items():
+        con.execute(f"CREATE TABLE {table} ({body})")
+    con.execute("PRAGMA user_version = 1")
+    con.execute(_REFERENCE_RUN_INSERT)
+    con.commit()
+    con.close()
+
+    env = capture_environment()
+    with ResultsDB(path) as db:
+        run = db.start_run(env, notes="mi355x", version="0.2")
+        db.record_many(run, _problem(), [
+            Measurement(label="kernelforge", status=STATUS_OK, config=KernelConfig("fake", MODE=0),
+                        tflops=1.0)])
+        (row,) = db.rows(operation="fake")
+        assert row["label"] == "kernelforge" and row["triton_version"] is None
+        assert [r["run_id"] for r in db.runs()] == [1, run]
+
+    con = sqlite3.connect(path)
+    ours = con.execute("SELECT sm_count, cu_count, hip_version, kernelforge_version, cuda_version "
+                       "FROM runs WHERE run_id = ?", (run,)).fetchone()
+    assert ours == (env.cu_count, env.cu_count, env.hip_version, "0.2", None)
+    con.execute(_REFERENCE_RUN_INSERT)  # the reference writing into the widened table
+    (read,) = con.execute(_REFERENCE_ROWS_SELECT).fetchall()
+    assert read[0] == "kernelforge" and read[-2] == env.cu_count
+    con.close()
+
+    fresh = tmp_path / "ours.db"
+    with ResultsDB(fresh) as db:
+        db.record_many(db.start_run(env), _problem(), [Measurement("torch_eager", STATUS_OK)])
+    con = sqlite3.connect(fresh)
+    con.execute(_REFERENCE_RUN_INSERT)
+    assert [r[0] for r in con.execute(_REFERENCE_ROWS_SELECT)] == ["torch_eager"]
+    con.close()
+
+
 def test_best_per_label_ignores_incorrect_rows(tmp_path):
     from kernelforge.benchmark.runner import summarize
     from kernelforge.testing import verify

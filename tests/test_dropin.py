@@ -48,6 +48,9 @@ SURFACE = [
     ("kernelforge.integration", "TransformerBlock", None),
     ("kernelforge.integration", "BlockConfig", None),
     ("kernelforge.integration", "benchmark_block", None),
+    ("kernelforge.integration.transformer", "BACKEND_KERNELFORGE", None),
+    ("kernelforge.integration.transformer", "BACKEND_TORCH", None),
+    ("kernelforge.integration.transformer", "BACKENDS", None),
     ("kernelforge.profiling", "profile_kernels", None),
     ("kernelforge.cli.main", "main", ["argv"]),
 ]

@@ -267,24 +267,24 @@ def _block(seed=0):
 
 @pytest.mark.parametrize("batch,seq", [(2, 128), (1, 1), (1, 7), (3, 5)])
 def test_block_backends_agree_on_one_set_of_weights(batch, seq):
-    from kernelforge.integration.transformer import BACKEND_KERNELO, BACKEND_TORCH
+    from kernelforge.integration.transformer import BACKEND_KERNELFORGE, BACKEND_TORCH
 
     block = _block()
     x = _randn(batch, seq, 256, dtype=torch.float16, seed=31).to(DEV)
     with torch.inference_mode():
         block.backend = BACKEND_TORCH
         expected = block(x)
-        block.backend = BACKEND_KERNELO
+        block.backend = BACKEND_KERNELFORGE
         actual = block(x)
     res = verify(expected.float().cpu(), actual.cpu(), dtype=torch.float16)
     assert res.passed, f"batch={batch} seq={seq}: {res.reason}"
 
 
 def test_block_resolves_configurations_once_per_shape():
-    from kernelforge.integration.transformer import BACKEND_KERNELO
+    from kernelforge.integration.transformer import BACKEND_KERNELFORGE
 
     block = _block()
-    block.backend = BACKEND_KERNELO
+    block.backend = BACKEND_KERNELFORGE
     x = _randn(1, 64, 256, dtype=torch.float16, seed=32).to(DEV)
     with torch.inference_mode():
         block(x)

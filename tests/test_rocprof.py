@@ -183,3 +183,70 @@ def test_profile_prices_each_dtype_against_its_own_mfma_peak(monkeypatch, capsys
     # 68,719,476,736 FLOP in 500 us = 137.4 TFLOP/s.
     tflops = 68_719_476_736 / 500e-6 / 1e12
     assert f"{tflops:.1f} TFLOP/s = {100 * tflops / float(peak):.1f}% of peak" in capsys.readouterr().out
+
+
+def _fake_passes(monkeypatch, results):
+    """Make rocprof.run's passes return ``results[name] = (rc, log)`` and write a
+    counter or trace file holding one GEMM dispatch, as rocprofv3 would."""
+    monkeypatch.setattr(rocprof, "rocprof_available", lambda: True)
+
+    def fake(command, timeout):
+        out_dir = command[command.index("-d") + 1]
+        name = command[command.index("-o") + 1]
+        from pathlib import Path
+
+        Path(out_dir).mkdir(parents=True, exist_ok=True)
+        if "--pmc" in command:
+            _counter_csv(Path(out_dir) / f"{name}_counter_collection.csv",
+                         [(4, GEMM, c, 1000.0) for c in command[command.index("--pmc") + 1:
+                                                               command.index("--output-format")]])
+        else:
+            with open(Path(out_dir) / f"{name}_kernel_trace.csv", "w", newline="") as fh:
+                w = csv.writer(fh)
+                w.writerow(TRACE_HEADER)
+                w.writerow(["KERNEL_DISPATCH", "Agent 1", 1, 0, 7, 4, 3, GEMM, 4, 5_000, 70_400,
+                            65536, 0, 128, 128, 40, 512, 1, 1, 131072, 1, 1])
+        return results[name]
+
+    monkeypatch.setattr(rocprof, "_run_pass", fake)
+
+
+def test_a_profiler_segfault_after_a_finished_program_is_reported_not_hidden(monkeypatch, tmp_path):
+    """rocprofv3 can end on SIGSEGV in its own teardown once the program it ran
+    has exited and its files are written. Such a pass is used, and the run
+    carries and prints what happened; the raw status is kept."""
+    import signal
+
+    segv = int(signal.SIGSEGV)
+    _fake_passes(monkeypatch, {
+        "trace": (0, f"...\n{rocprof.CHILD_DONE}\n"),
+        "fetch": (-segv, f"...\n{rocprof.CHILD_DONE}\n"),
+    })
+    run = rocprof.run(["python"], out_dir=tmp_path, passes=("trace", "fetch"))
+    assert run.ok and run.returncodes == [0, 0] and run.raw_returncodes == [0, -segv]
+    assert len(run.notes) == 1 and "SIGSEGV" in run.notes[0] and "'fetch'" in run.notes[0]
+    text = run.render(flops=1, algorithmic_bytes=1, peak_tflops=1, peak_gbps=1, cu_count=256,
+                      memory_bound=False)
+    assert "note: pass 'fetch': rocprofv3 exited on SIGSEGV" in text
+
+
+@pytest.mark.parametrize("status", (-11, 139))
+def test_a_profiler_segfault_before_the_program_finished_fails_the_profile(monkeypatch, tmp_path,
+                                                                           status):
+    """Without the child's completion line the same signal is a failure: the
+    pass's status stands and the profile is not ok, whatever the files hold."""
+    _fake_passes(monkeypatch, {"trace": (0, rocprof.CHILD_DONE), "mfma": (status, "partial")})
+    run = rocprof.run(["python"], out_dir=tmp_path, passes=("trace", "mfma"))
+    assert not run.ok and run.returncodes == [0, status]
+    assert "before the profiled program finished" in run.notes[0]
+
+
+def test_the_launch_once_child_prints_the_completion_line_last():
+    """The parent recognises a finished child by this line; it must be what
+    _launch_once prints after its measured launch has synchronised."""
+    import inspect
+
+    from kernelforge.cli import main as cli
+
+    src = inspect.getsource(cli._launch_once)
+    assert src.index("torch.cuda.synchronize") < src.index("print(CHILD_DONE")

@@ -100,3 +100,16 @@ def test_no_alloc_repeats_bitwise_and_refuses_oversized_splits():
                               y.data_ptr(), 8, n, k, k, 1, n, 1, n, 1, 0, too_many, 8, 32,
                               hip.stream_of(x8))
     assert rc == hip.KF_ERR_WORKSPACE and "static scratch" in hip.last_error()
+    # More column blocks than a workspace has counters: the scratch would be
+    # large enough, so both entry points refuse it the same way, without
+    # launching (the pointers are never dereferenced).
+    wide = hip.KF_WORKSPACE_COUNTERS + 1
+    codes = []
+    for entry in ("kf_gemv", "kf_gemv_no_alloc"):
+        args = [abi_code(torch.bfloat16), dx.data_ptr(), dw.data_ptr(), None, y.data_ptr(),
+                1, wide, k, k, 1, wide, 1, wide, 1, 0, 2, 8, 32]
+        if entry == "kf_gemv":
+            args += [None, 0]
+        codes.append(getattr(lib, entry)(*args, hip.stream_of(dx)))
+        assert "counters" in hip.last_error(), (entry, hip.last_error())
+    assert codes == [hip.KF_ERR_INVALID_ARGUMENT] * 2
