@@ -40,8 +40,14 @@ warm-up and K timed steps (the comparison's launches precede them).
 
 Each configuration's output is checked against torch on the same device with
 the reference's gate before it is timed. The CPU baseline is the oracle
-(oracle/ops.py, torch eager in fp32) timed on the host cores on a bounded
-slice of each workload.
+(oracle/ops.py, torch eager in fp32) timed on the host cores over each full
+workload, with the reference's CPU warm-up and iteration counts.
+
+``roofline.kernel_us`` / ``kernel_frac`` and ``roofline.traffic`` come from the
+committed rocprofv3 summaries in profiles/ (kernelforge.profiling.bench_profiles
+over a ``--marks`` run of this script); each is null, with the reason, when the
+summary was made from another library build (source digest) or another
+configuration than the one dispatch picks in this run.
 """
 
 from __future__ import annotations
@@ -248,45 +254,46 @@ class _BusySampler:
                 "min_pct": min(self.samples) if n else None}
 
 
-def _cpu_time(fn, seconds: float) -> tuple[float, int]:
-    """Mean seconds per call over at least ``seconds`` of calls (after one warm call)."""
-    fn()  # warm caches / thread pool
-    t0 = time.perf_counter()
-    iters = 0
-    while True:
-        fn()
-        iters += 1
-        elapsed = time.perf_counter() - t0
-        if elapsed >= seconds:
-            return elapsed / iters, iters
-
-
-def _traffic(name: str) -> float | None:
-    """HBM bytes per launch for ``name`` from the committed rocprofv3 counter summary.
-
-    ``profiles/hbm_traffic.json`` holds FETCH_SIZE + WRITE_SIZE per dispatch of each
-    configuration's kernel, scaled by what the same counters read for a copy of
-    known size; absent entries leave ``traffic`` null.
-    """
-    path = REPO / "profiles" / "hbm_traffic.json"
+def profile_entry(path: Path, name: str, config: dict | None, digest: str) -> tuple[dict | None, str | None]:
+    """The committed rocprofv3 summary of workload ``name`` (``profiles/kernel_trace.json``
+    or ``profiles/hbm_traffic.json``, written by kernelforge.profiling.bench_profiles), or
+    None and the reason it does not describe this run: no entry, another library build
+    (source digest), or a configuration dispatch no longer picks."""
     if not path.exists():
-        return None
-    entry = json.loads(path.read_text()).get("kernels", {}).get(name)
-    return None if entry is None else float(entry["traffic_bytes"])
-
-
-def _kernel_time(name: str, work: float, scale: float, peak: float) -> dict:
-    """Median kernel duration of ``name`` from the committed rocprofv3 kernel trace,
-    and the roofline fraction it gives (null when the trace has no such entry)."""
-    path = REPO / "profiles" / "kernel_trace.json"
-    entry = None
-    if path.exists():
-        entry = json.loads(path.read_text()).get("kernels", {}).get(name)
+        return None, f"{path.name} is missing"
+    doc = json.loads(path.read_text())
+    entry = doc.get("kernels", {}).get(name)
     if entry is None:
-        return {"kernel_us": None, "kernel_frac": None, "kernel_method": None}
+        return None, f"{path.name} has no entry for {name}"
+    if doc.get("library_digest") != digest:
+        return None, (f"{path.name} profiled library sources {doc.get('library_digest')}, "
+                      f"this run loaded {digest}")
+    if entry.get("config") != config:
+        return None, (f"{path.name} profiled configuration {entry.get('config')}, "
+                      f"dispatch picked {config} in this run")
+    return entry, None
+
+
+def _kernel_time(name: str, work: float, scale: float, peak: float, config: dict | None,
+                 digest: str) -> dict:
+    """Median kernel duration of ``name``'s kernel from the committed rocprofv3 trace and
+    the roofline fraction it gives; null, with the reason, when that trace does not
+    describe the kernel this run launched."""
+    entry, why = profile_entry(REPO / "profiles" / "kernel_trace.json", name, config, digest)
+    if entry is None:
+        return {"kernel_us": None, "kernel_frac": None, "kernel_method": None, "kernel_null_reason": why}
     us = float(entry["median_us"])
     return {"kernel_us": us, "kernel_frac": (work / (us * 1e-6)) / scale / peak,
-            "kernel_method": "median of the rocprofv3 kernel trace in profiles/kernel_trace.json"}
+            "kernel_name": entry["kernel"], "kernel_grid": entry["grid"],
+            "kernel_method": "median dispatch duration in profiles/kernel_trace.json (rocprofv3 "
+                             "kernel trace of this library build and configuration)"}
+
+
+def _traffic(name: str, config: dict | None, digest: str) -> tuple[float | None, str | None]:
+    """HBM bytes per launch of ``name``'s kernel from the committed FETCH_SIZE/WRITE_SIZE
+    summary (copy-calibrated), or None and the reason."""
+    entry, why = profile_entry(REPO / "profiles" / "hbm_traffic.json", name, config, digest)
+    return (None, why) if entry is None else (float(entry["traffic_bytes"]), None)
 
 
 def main(argv: list[str] | None = None) -> int:
@@ -298,6 +305,11 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--no-sustained", action="store_true",
                         help="skip the graph-captured sustained runs and the soak (profiling the "
                              "headline method)")
+    parser.add_argument("--marks", default=None,
+                        help="launch a marker kernel before each workload and write the workload "
+                             "list, configurations and library digest to this file, for "
+                             "kernelforge.profiling.bench_profiles to cut a rocprofv3 run into "
+                             "workloads")
     parser.add_argument("--soak-seconds", type=float, default=8.0,
                         help="seconds of back-to-back headline GEMM launches after the configs "
                              "(0 skips)")
@@ -323,6 +335,8 @@ def main(argv: list[str] | None = None) -> int:
     from kernelforge.testing import assert_verified, exact_fp32_matmul
 
     from kernelforge.kernels import get_operator
+    from kernelforge.profiling.bench_profiles import MARKER_STRIDE
+    from kernelforge.runtime import hip
     from kernelforge.runtime.dispatch import select_config
     from kernelforge.tuning.config import Problem
 
@@ -336,6 +350,16 @@ def main(argv: list[str] | None = None) -> int:
     steps, warmup = args.steps, args.warmup
     g = torch.Generator().manual_seed(0)
     results: dict[str, dict] = {}
+    digest = hip.source_digest()
+    marks: list[dict] = []
+
+    def mark(name, config, **extra):
+        """With --marks: an int8 fill of a size of its own ahead of the workload's
+        launches (the marker bench_profiles cuts a profile at), and its entry."""
+        if args.marks is None:
+            return
+        torch.full((MARKER_STRIDE * (len(marks) + 1),), 77, dtype=torch.int8, device=dev)
+        marks.append({"name": name, "config": config, **extra})
 
     def pick(operation, dtype, **dims):
         """The config dispatch would run: user cache, packaged winners, default."""
@@ -345,6 +369,8 @@ def main(argv: list[str] | None = None) -> int:
 
     def record(name, fns, work, unit, peak, extra=None):
         scale = 1e12 if unit == "TFLOP/s" else 1e9
+        config = (extra or {}).get("kernel_config")
+        traffic, traffic_why = _traffic(name, config, digest)
         flushed = _time_flushed(fns[0], steps, warmup, flush)
         mean_ms = float(np.mean(flushed))
         rate = (work / (mean_ms * 1e-3)) / scale
@@ -370,13 +396,16 @@ def main(argv: list[str] | None = None) -> int:
                 "peak": peak,
                 "unit": "TFLOP/s" if unit == "TFLOP/s" else "GB/s",
                 "frac": rate / peak,
-                "traffic": _traffic(name),
+                "traffic": traffic,
                 # Kernel time without the per-launch dispatch gap: the median
                 # kernel duration of the same workload in the committed rocprofv3
-                # kernel trace (profiles/kernel_trace.json).
-                **_kernel_time(name, work, scale, peak),
+                # kernel trace (profiles/kernel_trace.json), if it profiled this
+                # library build and this configuration.
+                **_kernel_time(name, work, scale, peak, config, digest),
             },
         }
+        if traffic is None:
+            entry["roofline"]["traffic_null_reason"] = traffic_why
         if extra:
             entry.update(extra)
         results[name] = entry
@@ -402,23 +431,27 @@ def main(argv: list[str] | None = None) -> int:
     gamma = 1.0 + 0.1 * torch.randn(4096, generator=g)
     dx, dgamma = x.to(dev), gamma.to(dev)
     soft = {}
+    soft_host = {}  # the CPU baseline runs on the same inputs
     for cols in (4096, 11008):
         s = 3.0 * torch.randn(8192, cols, generator=g)
         s[torch.randperm(8192, generator=g)[:82]] += 60.0
-        soft[cols] = s.to(torch.float16).to(dev)
+        soft_host[cols] = s.to(torch.float16)
+        soft[cols] = soft_host[cols].to(dev)
         del s
     M, N, K = 2048, 4096, 4096
     a = (torch.randn(M, K, generator=g) / K**0.5).to(torch.float16).to(dev)
     b = (torch.randn(K, N, generator=g) / K**0.5).to(torch.float16).to(dev)
     FM, FN, FK = 4096, 11008, 4096
-    fx = (torch.randn(FM, FK, generator=g) / FK**0.5).to(torch.float16).to(dev)
-    fw = (torch.randn(FK, FN, generator=g) / FK**0.5).to(torch.float16).to(dev)
-    fb = (0.02 * torch.randn(FN, generator=g)).to(torch.float16).to(dev)
+    fx_host = (torch.randn(FM, FK, generator=g) / FK**0.5).to(torch.float16)
+    fw_host = (torch.randn(FK, FN, generator=g) / FK**0.5).to(torch.float16)
+    fb_host = (0.02 * torch.randn(FN, generator=g)).to(torch.float16)
+    fx, fw, fb = fx_host.to(dev), fw_host.to(dev), fb_host.to(dev)
     vx = (torch.rand(1, 4096, generator=g) * 2 - 1).to(torch.bfloat16).to(dev)
     vw = (torch.rand(4096, 11008, generator=g) * 2 - 1).to(torch.bfloat16).to(dev)
     VN = 1 << 26
-    va = torch.randn(VN, generator=g).to(dev)
-    vb = torch.randn(VN, generator=g).to(dev)
+    va_host = torch.randn(VN, generator=g)
+    vb_host = torch.randn(VN, generator=g)
+    va, vb = va_host.to(dev), vb_host.to(dev)
     WR, WC = 4096, 32768
     wx = torch.randn(WR, WC, generator=g).to(torch.float16).to(dev)
     wg = (1.0 + 0.1 * torch.randn(WC, generator=g)).to(torch.float16).to(dev)
@@ -427,12 +460,16 @@ def main(argv: list[str] | None = None) -> int:
     # --- calibration: a plain device-to-device copy of 1 GiB (read + write) -----
     src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
     dst = [torch.empty_like(src) for _ in range(2)]
+    mark("hbm_copy_1GiB", None, kernel_hint="copy", copy_bytes=src.numel() * 4,
+         algorithmic_bytes=2 * src.numel() * 4)
     record("hbm_copy_1GiB", [lambda i=i: dst[i].copy_(src) for i in range(2)],
            2 * src.numel() * 4, "GB/s", hbm)
     del src, dst
 
     # --- config 1: RMSNorm fp32 [4096,4096], eps=1e-6 ----------------------------
     cfg, src = pick("rmsnorm", "fp32", rows=4096, cols=4096)
+    mark("rmsnorm_fp32_4096x4096", src["kernel_config"],
+         algorithmic_bytes=metrics.rmsnorm_bytes(4096, 4096, 4))
     assert_verified(rmsnorm_reference(dx, dgamma, eps=1e-6),
                     rmsnorm(dx, dgamma, eps=1e-6, config=cfg), context="rmsnorm config 1")
     work = metrics.rmsnorm_bytes(4096, 4096, 4)
@@ -446,6 +483,8 @@ def main(argv: list[str] | None = None) -> int:
     for cols in (4096, 11008):
         ds = soft.pop(cols)
         cfg, src = pick("softmax", "fp16", rows=8192, cols=cols)
+        mark(f"softmax_fp16_8192x{cols}", src["kernel_config"],
+             algorithmic_bytes=metrics.softmax_bytes(8192, cols, 2))
         out = softmax(ds, config=cfg)
         assert torch.isfinite(out).all()
         assert_verified(torch.softmax(ds.float(), -1), out, dtype=torch.float16,
@@ -459,6 +498,8 @@ def main(argv: list[str] | None = None) -> int:
 
     # --- config 3: GEMM fp16 2048x4096x4096 (headline) -----------------------------
     gcfg, src = pick("matmul", "fp16", M=M, N=N, K=K)
+    mark("gemm_fp16_2048x4096x4096", src["kernel_config"],
+         algorithmic_bytes=metrics.matmul_bytes(M, N, K, 2))
     with exact_fp32_matmul():
         assert_verified(torch.matmul(a.float(), b.float()), matmul(a, b, config=gcfg),
                         dtype=torch.float16, context="gemm config 3")
@@ -477,6 +518,8 @@ def main(argv: list[str] | None = None) -> int:
 
     # --- config 4: fused linear fp16 4096x11008x4096 + bias + GELU(tanh) -----------
     fcfg, src = pick("fused_linear", "fp16", M=FM, N=FN, K=FK)
+    mark("fused_linear_fp16_4096x11008x4096", src["kernel_config"],
+         algorithmic_bytes=metrics.fused_linear_bytes(FM, FN, FK, 2, fused=True))
     assert_verified(linear_gelu_reference(fx, fw, fb), fused_linear_gelu(fx, fw, fb, config=fcfg),
                     context="fused linear config 4")
     mine, tu = _time_interleaved(lambda: fused_linear_gelu(fx, fw, fb, config=fcfg),
@@ -495,6 +538,8 @@ def main(argv: list[str] | None = None) -> int:
 
     # --- config 5a: decode GEMV bf16 1x11008x4096 ----------------------------------
     vcfg, src = pick("matmul", "bf16", M=1, N=11008, K=4096)
+    mark("gemv_bf16_1x11008x4096", src["kernel_config"],
+         algorithmic_bytes=metrics.matmul_bytes(1, 11008, 4096, 2))
     assert_verified(torch.matmul(vx.float(), vw.float()), matmul(vx, vw, config=vcfg),
                     dtype=torch.bfloat16, context="gemv config 5a")
     work = metrics.matmul_bytes(1, 11008, 4096, 2)
@@ -514,6 +559,8 @@ def main(argv: list[str] | None = None) -> int:
     from kernelforge.kernels.vector_add import vector_add
 
     acfg, src = pick("vector_add", "fp32", n=VN)
+    mark("vector_add_fp32_67108864", src["kernel_config"],
+         algorithmic_bytes=metrics.vector_add_bytes(VN, 4))
     assert torch.equal(vector_add(va, vb, config=acfg), va + vb), "vector_add must be bit-exact"
     work = metrics.vector_add_bytes(VN, 4)
     mine, ta = _time_interleaved(lambda: vector_add(va, vb, config=acfg), lambda: va + vb, steps,
@@ -527,6 +574,8 @@ def main(argv: list[str] | None = None) -> int:
     del cp, va, vb
 
     wcfg, src = pick("rmsnorm", "fp16", rows=WR, cols=WC)
+    mark(f"rmsnorm_two_pass_fp16_{WR}x{WC}", src["kernel_config"],
+         algorithmic_bytes=metrics.rmsnorm_bytes(WR, WC, 2))
     assert_verified(rmsnorm_reference(wx, wg, eps=1e-6), rmsnorm(wx, wg, eps=1e-6, config=wcfg),
                     context="two-pass rmsnorm")
     work = metrics.rmsnorm_bytes(WR, WC, 2)
@@ -560,55 +609,67 @@ def main(argv: list[str] | None = None) -> int:
              f"{soak['value']:.1f} TFLOP/s")
         del cp
 
-    # --- CPU baseline: the oracle on the host cores, bounded slices ----------------
-    # About 4 s of calls per workload (about 20 s in all), on bounded slices of the
-    # same inputs; the headline is the GEMM slice.
+    # --- CPU baseline: the oracle on the host cores, full workloads ----------------
+    # The reference's CPU timing (kernelforge/benchmark/runner.py:153-166): perf_counter
+    # around each call after the warm-up, median of the calls; 1 warm-up and 3 calls
+    # for the GEMM and the fused linear, 3 and 20 for the row kernels, the GEMV and
+    # vector_add. Same seeded inputs as the GPU run, every workload at full size.
     cpu = None
     if not args.no_cpu_baseline:
         from oracle import ops
 
         cores = host_cores()
         torch.set_num_threads(cores)
-        budget = 4.0
 
-        def cpu_entry(fn, work, unit, sample):
-            secs, iters = _cpu_time(fn, budget)
+        def cpu_entry(fn, work, unit, sample, warmup, iterations):
+            for _ in range(warmup):
+                fn()
+            secs = []
+            for _ in range(iterations):
+                t0 = time.perf_counter()
+                fn()
+                secs.append(time.perf_counter() - t0)
+            med = float(np.median(secs))
             scale = 1e12 if unit == "TFLOP/s" else 1e9
-            return {"value": work / secs / scale, "unit": unit, "cores": cores, "kind": "port",
-                    "sample": f"{sample}; mean of {iters} calls over {secs * iters:.1f} s"}
+            _log(f"cpu baseline: {sample}: {med * 1e3:.1f} ms per call on {cores} threads")
+            return {"value": work / med / scale, "unit": unit, "cores": cores, "kind": "port",
+                    "timer": "perf_counter", "median_ms": med * 1e3,
+                    "sample": f"{sample}, full workload; median of {iterations} calls after "
+                              f"{warmup} warm-up"}
 
-        rows = 256
-        ca, cb = a[:rows].cpu(), b.cpu()
-        cpu = cpu_entry(lambda: ops.matmul_ref(ca, cb), metrics.matmul_flops(rows, N, K), "TFLOP/s",
-                        f"oracle matmul_ref (torch fp32 on CPU) on A[:{rows}] @ B, {rows}x{N}x{K}")
+        ca, cb = a.cpu(), b.cpu()
+        cpu = cpu_entry(lambda: ops.matmul_ref(ca, cb), metrics.matmul_flops(M, N, K), "TFLOP/s",
+                        f"oracle matmul_ref (torch fp32 on CPU), {M}x{N}x{K} fp16 inputs", 1, 3)
         results["gemm_fp16_2048x4096x4096"]["cpu_baseline"] = cpu
+        del ca, cb
+        results["fused_linear_fp16_4096x11008x4096"]["cpu_baseline"] = cpu_entry(
+            lambda: ops.linear_gelu_ref(fx_host, fw_host, fb_host), metrics.matmul_flops(FM, FN, FK),
+            "TFLOP/s", f"oracle linear_gelu_ref, {FM}x{FN}x{FK} fp16 inputs", 1, 3)
         results["rmsnorm_fp32_4096x4096"]["cpu_baseline"] = cpu_entry(
             lambda: ops.rmsnorm_ref(x, gamma, 1e-6), metrics.rmsnorm_bytes(4096, 4096, 4), "GB/s",
-            "oracle rmsnorm_ref, full [4096,4096] fp32")
+            "oracle rmsnorm_ref, [4096,4096] fp32", 3, 20)
         for cols in (4096, 11008):
-            cs = (3.0 * torch.randn(1024, cols, generator=g)).to(torch.float16)
+            cs = soft_host[cols]
             results[f"softmax_fp16_8192x{cols}"]["cpu_baseline"] = cpu_entry(
-                lambda cs=cs: ops.softmax_ref(cs), metrics.softmax_bytes(1024, cols, 2), "GB/s",
-                f"oracle softmax_ref on [1024,{cols}] fp16")
+                lambda cs=cs: ops.softmax_ref(cs), metrics.softmax_bytes(8192, cols, 2), "GB/s",
+                f"oracle softmax_ref, [8192,{cols}] fp16 with the +60 rows", 3, 20)
         cvx, cvw = vx.cpu(), vw.cpu()
         results["gemv_bf16_1x11008x4096"]["cpu_baseline"] = cpu_entry(
             lambda: ops.matmul_ref(cvx, cvw), metrics.matmul_bytes(1, 11008, 4096, 2), "GB/s",
-            "oracle matmul_ref, full 1x11008x4096 bf16")
-        fxs = (torch.randn(64, FK, generator=g) / 64).to(torch.float16)
-        fws = (torch.randn(FK, FN, generator=g) / 64).to(torch.float16)
-        fbs = fb.cpu()
-        results["fused_linear_fp16_4096x11008x4096"]["cpu_baseline"] = cpu_entry(
-            lambda: ops.linear_gelu_ref(fxs, fws, fbs), metrics.matmul_flops(64, FN, FK), "TFLOP/s",
-            f"oracle linear_gelu_ref on X[:64], 64x{FN}x{FK}")
-        ca2 = torch.randn(1 << 22, generator=g)
-        cb2 = torch.randn(1 << 22, generator=g)
+            "oracle matmul_ref, 1x11008x4096 bf16", 3, 20)
         results["vector_add_fp32_67108864"]["cpu_baseline"] = cpu_entry(
-            lambda: ops.vector_add_ref(ca2, cb2), metrics.vector_add_bytes(1 << 22, 4), "GB/s",
-            "oracle vector_add_ref on 4194304 fp32 elements")
-        cwx, cwg = wx[:64].cpu(), wg.cpu()
+            lambda: ops.vector_add_ref(va_host, vb_host), metrics.vector_add_bytes(VN, 4), "GB/s",
+            f"oracle vector_add_ref, {VN} fp32 elements", 3, 20)
+        cwx, cwg = wx.cpu(), wg.cpu()
         results[f"rmsnorm_two_pass_fp16_{WR}x{WC}"]["cpu_baseline"] = cpu_entry(
-            lambda: ops.rmsnorm_ref(cwx, cwg, 1e-6), metrics.rmsnorm_bytes(64, WC, 2), "GB/s",
-            f"oracle rmsnorm_ref on x[:64], 64x{WC} fp16")
+            lambda: ops.rmsnorm_ref(cwx, cwg, 1e-6), metrics.rmsnorm_bytes(WR, WC, 2), "GB/s",
+            f"oracle rmsnorm_ref, [{WR},{WC}] fp16", 3, 20)
+
+    if args.marks is not None:
+        Path(args.marks).parent.mkdir(parents=True, exist_ok=True)
+        Path(args.marks).write_text(json.dumps({"library_digest": digest, "argv": sys.argv,
+                                                "workloads": marks}, indent=1) + "\n")
+        _log(f"marks: {len(marks)} workloads -> {args.marks}")
 
     line = {
         "metric": METRIC,

@@ -84,6 +84,11 @@ enum {
 /* Library identification: ABI version and the offload target it was built for. */
 int kf_abi_version(void);
 const char* kf_build_target(void);
+/* First 16 hex digits of SHA-256 over the sources, tile lists and flags the
+ * library was built from (kernelforge/build.py source_digest): profiles and
+ * measurements record it to name the code they ran. No counterpart in the
+ * reference (Triton compiles from the Python source it ships). */
+const char* kf_source_digest(void);
 
 /* Message describing the last failure on the calling thread ("" if none). */
 const char* kf_last_error(void);

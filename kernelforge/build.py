@@ -15,6 +15,7 @@ Always recompiles: a stale library must never pass for the current sources.
 from __future__ import annotations
 
 import argparse
+import hashlib
 import os
 import shutil
 import subprocess
@@ -84,6 +85,25 @@ def generate() -> list[tuple[int, int, int, Path]]:
     return units
 
 
+def source_digest() -> str:
+    """First 16 hex digits of SHA-256 over everything a build compiles: the
+    sources under csrc/ and include/, the GEMM tile lists the search space
+    generates, and the compiler flags. Built into the library
+    (``kf_source_digest``), so a profile or measurement can name the exact
+    code it ran, and identical for every rebuild of the same tree."""
+    sys.path.insert(0, str(REPO))
+    from kernelforge.tuning.search import gemm_instantiations
+
+    h = hashlib.sha256()
+    for path in sorted([*CSRC.iterdir(), *INCLUDE.glob("*.h")]):
+        if path.is_file():
+            h.update(path.name.encode() + b"\0" + path.read_bytes() + b"\0")
+    for direct in (0, 1):
+        h.update(repr(sorted(gemm_instantiations(direct=direct).items())).encode())
+    h.update(" ".join(HIP_FLAGS).encode())
+    return h.hexdigest()[:16]
+
+
 def _compile(src: Path, obj: Path, extra: list[str]) -> tuple[Path, float, str]:
     t0 = time.perf_counter()
     cmd = [HIPCC, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", f"-I{GEN}", *extra, "-c", str(src), "-o", str(obj)]
@@ -106,8 +126,9 @@ def build(jobs: int | None = None, verbose: bool = True) -> Path:
         shutil.rmtree(obj_dir)
     obj_dir.mkdir(parents=True)
     units = generate()
+    digest = source_digest()
     tasks = [
-        (CSRC / "abi.hip", obj_dir / "abi.o", []),
+        (CSRC / "abi.hip", obj_dir / "abi.o", [f'-DKF_SOURCE_DIGEST="{digest}"']),
         (CSRC / "rows.hip", obj_dir / "rows.o", []),
         (CSRC / "gemv.hip", obj_dir / "gemv.o", []),
         (CSRC / "wide_rows.hip", obj_dir / "wide_rows.o", []),
@@ -138,7 +159,7 @@ def build(jobs: int | None = None, verbose: bool = True) -> Path:
     os.replace(tmp, LIBRARY)
     if verbose:
         print(
-            f"built {LIBRARY.relative_to(REPO)}: {len(tasks)} units "
+            f"built {LIBRARY.relative_to(REPO)} (sources {digest}): {len(tasks)} units "
             f"({len(units)} GEMM chunks) in {time.perf_counter() - t0:.1f}s with {jobs} jobs"
         )
     return LIBRARY

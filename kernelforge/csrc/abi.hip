@@ -33,6 +33,12 @@ extern "C" int kf_abi_version(void) { return 5; }
 
 extern "C" const char* kf_build_target(void) { return "gfx950"; }
 
+// The build passes the digest of the sources it compiled (kernelforge/build.py).
+#ifndef KF_SOURCE_DIGEST
+#define KF_SOURCE_DIGEST "unknown"
+#endif
+extern "C" const char* kf_source_digest(void) { return KF_SOURCE_DIGEST; }
+
 extern "C" const char* kf_last_error(void) { return kf::g_last_error; }
 
 extern "C" int kf_stream_capture_id(void* stream, unsigned long long* id) {

@@ -98,6 +98,7 @@ _sz = ctypes.c_size_t
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "kf_abi_version": (_int, []),
     "kf_build_target": (ctypes.c_char_p, []),
+    "kf_source_digest": (ctypes.c_char_p, []),
     "kf_last_error": (ctypes.c_char_p, []),
     "kf_stream_capture_id": (_int, [_vp, ctypes.POINTER(ctypes.c_ulonglong)]),
     "kf_gemm": (
@@ -190,6 +191,11 @@ def is_loaded() -> bool:
 def last_error() -> str:
     raw = load().kf_last_error()
     return raw.decode(errors="replace") if raw else ""
+
+
+def source_digest() -> str:
+    """The digest of the sources the loaded library was built from (``kf_source_digest``)."""
+    return load().kf_source_digest().decode()
 
 
 def check(rc: int, what: str) -> None:

@@ -35,7 +35,8 @@ def lib():
 
 def test_header_declares_the_expected_entry_points():
     assert _declared() == {
-        "kf_abi_version", "kf_build_target", "kf_last_error", "kf_stream_capture_id",
+        "kf_abi_version", "kf_build_target", "kf_source_digest", "kf_last_error",
+        "kf_stream_capture_id",
         "kf_gemm", "kf_gemm_has_variant", "kf_gemm_variant_count", "kf_gemm_variant_info",
         "kf_gemm_split_k", "kf_gemm_workspace_bytes", "kf_gemm_concurrent_tiles",
         "kf_gemv", "kf_gemv_workspace_bytes", "kf_gemv_no_alloc", "kf_softmax", "kf_rmsnorm",
@@ -53,6 +54,17 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 def test_identification(lib):
     assert lib.kf_abi_version() == hip.ABI_VERSION == 5
     assert lib.kf_build_target() == b"gfx950"
+
+
+def test_the_library_is_built_from_the_sources_in_the_tree(lib):
+    """The digest the build compiled in is the digest of today's sources, tile
+    lists and flags: a stale library (sources edited, not rebuilt) fails here,
+    and profiles keyed on the digest can only describe this code."""
+    from kernelforge import build
+
+    digest = hip.source_digest()
+    assert len(digest) == 16 and int(digest, 16) >= 0
+    assert digest == build.source_digest()
 
 
 def test_a_library_of_another_abi_version_is_refused(tmp_path):

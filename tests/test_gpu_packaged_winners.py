@@ -92,3 +92,86 @@ def test_packaged_winner_passes_the_gate_at_its_shape(op, dt, shape, cfg):
     res = verify(ref, out, dtype=dtype)
     print(f"  max normalised error {res.error:.3g} (threshold {res.threshold:g})", flush=True)
     assert res.passed, res.reason
+
+
+# --- the CPU oracle, once per tile family ---------------------------------------------
+
+
+def _families():
+    """One entry per (operation, dtype, B layout, configuration): the shipped
+    tile families, each with the first shape that ships it."""
+    seen = {}
+    for op, dt, shape, cfg in _entries():
+        layout = shape.partition("+")[2]
+        seen.setdefault((op, dt, layout, json.dumps(cfg, sort_keys=True)), (op, dt, shape, cfg))
+    return list(seen.values())
+
+
+def _small(op, shape, cfg):
+    """A small shape on which ``cfg`` still runs its own kernel: ragged against
+    the tile where the pipeline allows, 16-byte multiples of N and K kept for
+    the direct pipeline, the row width kept for the row kernels."""
+    key, _, layout = shape.partition("+")
+    dims = [int(v) for v in key.split("x")]
+    if op in ("matmul", "fused_linear"):
+        m, n, k = dims
+        if cfg.get("GEMV"):
+            return (m, min(n, 1032), min(k, 520)), layout
+        bm, bn = cfg["BLOCK_M"], cfg["BLOCK_N"]
+        return (min(m, 2 * bm + 17), min(n, 2 * bn + 24), min(k, 264)), layout
+    if op in ("softmax", "rmsnorm"):
+        return (min(dims[0], 64), dims[1]), layout
+    return (min(dims[0], 100003),), layout
+
+
+@pytest.mark.parametrize("op,dt,shape,cfg", _families(),
+                         ids=[f"{op}-{dt}-{shape}-{i}" for i, (op, dt, shape, _) in enumerate(_families())])
+def test_packaged_tile_family_matches_the_cpu_oracle(op, dt, shape, cfg):
+    """Every shipped configuration, on a small shape of its operation, against
+    oracle/ops.py on the CPU (the restatement of the reference's PyTorch
+    references) at the reference's per-dtype thresholds."""
+    from oracle import ops
+
+    dtype = DTYPES[dt]
+    config = KernelConfig(op, **cfg)
+    dims, layout = _small(op, shape, cfg)
+    print(f"{op} {dt} {dims}{'+' + layout if layout else ''} {cfg}", flush=True)
+    g = torch.Generator().manual_seed(sum(dims) + 11)
+    if op in ("matmul", "fused_linear"):
+        from kernelforge.kernels.fused_linear import fused_linear_gelu
+        from kernelforge.kernels.matmul import matmul
+
+        m, n, k = dims
+        a = (torch.rand(m, k, generator=g) * 2 - 1).to(dtype)
+        b = ((torch.rand(k, n, generator=g) * 2 - 1) * k**-0.5).to(dtype)
+        db = b.t().contiguous().to(DEV).t() if layout == "bt" else b.to(DEV)
+        if op == "matmul":
+            ref, out = ops.matmul_ref(a, b), matmul(a.to(DEV), db, config=config)
+        else:
+            bias = ((torch.rand(n, generator=g) * 2 - 1) * 0.5).to(dtype)
+            ref = ops.linear_gelu_ref(a, b, bias)
+            out = fused_linear_gelu(a.to(DEV), db, bias.to(DEV), config=config)
+    elif op == "softmax":
+        from kernelforge.kernels.softmax import softmax
+
+        x = (3.0 * torch.randn(*dims, generator=g)).to(dtype)
+        ref, out = ops.softmax_ref(x), softmax(x.to(DEV), config=config)
+    elif op == "rmsnorm":
+        from kernelforge.kernels.rmsnorm import rmsnorm
+
+        x = torch.randn(*dims, generator=g).to(dtype)
+        gamma = (1.0 + 0.1 * torch.randn(dims[1], generator=g)).to(dtype)
+        ref = ops.rmsnorm_ref(x, gamma, 1e-6)
+        out = rmsnorm(x.to(DEV), gamma.to(DEV), eps=1e-6, config=config)
+    elif op == "vector_add":
+        from kernelforge.kernels.vector_add import vector_add
+
+        x, y = torch.randn(dims[0], generator=g).to(dtype), torch.randn(dims[0], generator=g).to(dtype)
+        got = vector_add(x.to(DEV), y.to(DEV), config=config).cpu()
+        assert torch.equal(got, ops.vector_add_ref(x, y))  # correctly rounded: bit for bit
+        return
+    else:
+        pytest.fail(f"no oracle for {op}")
+    res = verify(ref.float(), out.cpu().float(), dtype=dtype)
+    print(f"  max normalised error {res.error:.3g} (threshold {res.threshold:g})", flush=True)
+    assert res.passed, res.reason

@@ -494,6 +494,42 @@ def test_edge_shapes_guard_band(m, n, k, cfg):
     _gate(ops.matmul_ref(a, b).float(), inside, torch.bfloat16, f"{cfg} {m}x{n}x{k}")
 
 
+@pytest.mark.parametrize("op", ("matmul", "fused_linear"))
+@pytest.mark.parametrize("m,n,k", [(1023, 4097, 127), (1, 7, 3)])
+def test_edge_shapes_guard_band_with_the_configuration_dispatch_picks(m, n, k, op):
+    """BASELINE configs 5b/5c run as the entry points run them without
+    config=: the configuration dispatch picks (shipped winner or heuristic),
+    launched by the entry points' own launcher into C inside a NaN guard band.
+    The band stays NaN, every element of C is finite and within the gate, and
+    C equals the entry point's own output bit for bit."""
+    from kernelforge.kernels.fused_linear import fused_linear_gelu
+    from kernelforge.kernels.matmul import default_gemm_config, launch_gemm, matmul
+
+    g = torch.Generator().manual_seed(m + n + k)
+    a = (torch.rand(m, k, generator=g) * 2 - 1).to(torch.bfloat16)
+    b = (torch.rand(k, n, generator=g) * 2 - 1).to(torch.bfloat16)
+    bias = (torch.rand(n, generator=g) * 2 - 1).to(torch.bfloat16) if op == "fused_linear" else None
+    da, db = a.to(DEV), b.to(DEV)
+    dbias = bias.to(DEV) if bias is not None else None
+    cfg = default_gemm_config(op, da, db)
+    print(f"{op} {m}x{n}x{k} bf16: dispatch picks {dict(cfg)}", flush=True)
+    pitch, pad = n + 9, 8
+    buf = torch.full(((m + 2 * pad) * pitch,), float("nan"), dtype=torch.bfloat16, device=DEV)
+    out = buf.view(m + 2 * pad, pitch)[pad : pad + m, :n]
+    launch_gemm(da, db, dbias, out, cfg)
+    own = matmul(da, db) if bias is None else fused_linear_gelu(da, db, dbias)
+    torch.cuda.synchronize()
+    host = buf.cpu().view(m + 2 * pad, pitch)
+    guard = torch.ones_like(host, dtype=torch.bool)
+    guard[pad : pad + m, :n] = False
+    assert torch.isnan(host[guard].float()).all(), "kernel wrote outside C"
+    inside = host[pad : pad + m, :n]
+    assert torch.isfinite(inside.float()).all()
+    assert torch.equal(inside.view(torch.int16), own.cpu().view(torch.int16))
+    ref = ops.matmul_ref(a, b) if bias is None else ops.linear_gelu_ref(a, b, bias)
+    _gate(ref.float(), inside.float(), torch.bfloat16, f"{op} dispatched {dict(cfg)} {m}x{n}x{k}")
+
+
 # --- HIP graph capture -------------------------------------------------------------
 
 
