@@ -41,16 +41,16 @@ from kernelforge.profiling.rocprof import (
     parse_trace_csv,
 )
 
-#: The marker: torch's fill kernel on int8 ("signed char"; mangled "IaE").
-MARKER_FILL = "FillFunctor"
-MARKER_TYPES = ("signed char", "FillFunctorIa")
+#: The marker: torch's fill kernel on int8, as rocprofv3 names it demangled
+#: or mangled ("a" is signed char; uint8 fills, "unsigned char" / "h", are not markers).
+MARKER_NAMES = ("FillFunctor<signed char>", "FillFunctorIaE")
 
 #: Elements of the i-th marker fill: (i + 1) * MARKER_STRIDE int8 values.
 MARKER_STRIDE = 1 << 16
 
 
 def is_marker(kernel: str) -> bool:
-    return MARKER_FILL in kernel and any(t in kernel for t in MARKER_TYPES)
+    return any(name in kernel for name in MARKER_NAMES)
 
 
 def split_workloads(dispatches: list[Dispatch], names: list[str]) -> dict[str, list[Dispatch]]:
@@ -149,6 +149,55 @@ def summarize_traffic(marks: dict, fetch_csv: str | Path, write_csv: str | Path,
             "kernels": kernels}
 
 
+def summarize_counters(marks: dict, csv_path: str | Path) -> dict[str, dict]:
+    """Per workload: the median per dispatch of every counter the pass collected."""
+    names = [w["name"] for w in marks["workloads"]]
+    segments = split_workloads(parse_counter_csv(csv_path), names)
+    out = {}
+    for w in marks["workloads"]:
+        ds = workload_kernel(segments[w["name"]], w.get("kernel_hint"))
+        if not ds:
+            raise ValueError(f"workload {w['name']}: no dispatch of its kernel in {csv_path}")
+        out[w["name"]] = {"kernel": ds[0].kernel, "grid": ds[0].grid, "config": w.get("config"),
+                          "dispatches": len(ds),
+                          "counters": {c: statistics.median(d.counters[c] for d in ds)
+                                       for c in sorted(ds[0].counters)}}
+    return out
+
+
+def counters_markdown(doc: dict, durations: dict[str, float], cu_count: int = 256) -> str:
+    """Counter medians per workload; with SQ_BUSY_CU_CYCLES and a kernel-trace
+    duration, the shader clock; with SQ_VALU_MFMA_BUSY_CYCLES too, the share of
+    SIMD busy cycles the matrix cores worked (four SIMDs per CU)."""
+    names = sorted({c for e in doc["kernels"].values() for c in e["counters"]})
+    head = ["workload", "dispatches", *names, "shader clock GHz", "MFMA busy / (4 x busy CU)"]
+    rows = []
+    for n, e in doc["kernels"].items():
+        c = e["counters"]
+        busy, mfma, us = c.get("SQ_BUSY_CU_CYCLES"), c.get("SQ_VALU_MFMA_BUSY_CYCLES"), durations.get(n)
+        clock = f"{busy / cu_count / (us * 1e3):.2f}" if busy and us else "-"
+        share = f"{100 * mfma / (4 * busy):.1f}%" if busy and mfma else "-"
+        rows.append("| " + " | ".join([n, str(e["dispatches"]), *(f"{c.get(k, 0):,.0f}" for k in names),
+                                       clock, share]) + " |")
+    cmds = "\n".join(doc["commands"])
+    return f"""# Hardware counters of every bench.py workload (rocprofv3 --pmc)
+
+Counter passes over the same bench command, then the summary (repository root, one MI355X):
+
+```
+{cmds}
+```
+
+Library source digest: `{doc['library_digest']}`. Medians per dispatch of each workload's kernel,
+found between its markers as for the kernel trace. Counters are summed over the chip: busy CU
+cycles over the 256 CUs, MFMA busy cycles over the 1024 SIMDs. The shader clock is busy cycles per
+CU over the median kernel-trace duration (kernel_trace.json, a separate run of the same tree).
+
+| {" | ".join(head)} |
+|{"---|" * len(head)}
+""" + "\n".join(rows) + "\n"
+
+
 def _short(name: str, width: int = 90) -> str:
     return name if len(name) <= width else name[: width - 3] + "..."
 
@@ -215,6 +264,11 @@ def main(argv: list[str] | None = None) -> int:
                    help="command line(s) that produced the trace, recorded in the summary")
     p.add_argument("--traffic-command", action="append", default=[],
                    help="command lines that produced the counter passes")
+    p.add_argument("--pmc", action="append", default=[],
+                   help="*_counter_collection.csv of any other counter pass (repeatable): "
+                        "per-workload medians go to bench_counters.json")
+    p.add_argument("--pmc-command", action="append", default=[],
+                   help="command lines that produced the --pmc passes")
     p.add_argument("--out", default="profiles")
     args = p.parse_args(argv)
     marks = load_marks(args.marks)
@@ -234,6 +288,22 @@ def main(argv: list[str] | None = None) -> int:
                **summarize_traffic(marks, args.fetch, args.write)}
         (out / "hbm_traffic.json").write_text(json.dumps(doc, indent=1) + "\n")
         (out / "hbm_traffic_bench_workloads.md").write_text(traffic_markdown(doc))
+    if args.pmc:
+        merged: dict[str, dict] = {}
+        for path in args.pmc:
+            for name, entry in summarize_counters(marks, path).items():
+                merged.setdefault(name, {**entry, "counters": {}})["counters"].update(entry["counters"])
+        me_pmc = me + "".join(f" --pmc {p}" for p in args.pmc)
+        doc = {"commands": [*args.pmc_command, me_pmc], "library_digest": marks["library_digest"],
+               "kernels": merged}
+        trace_json = out / "kernel_trace.json"
+        durations = {}
+        if trace_json.exists():
+            traced = json.loads(trace_json.read_text())
+            if traced.get("library_digest") == marks["library_digest"]:
+                durations = {n: e["median_us"] for n, e in traced["kernels"].items()}
+        (out / "bench_counters.json").write_text(json.dumps(doc, indent=1) + "\n")
+        (out / "bench_counters_workloads.md").write_text(counters_markdown(doc, durations))
     return 0
 
 

@@ -96,6 +96,7 @@ def test_markers_cut_the_run_and_each_workload_takes_its_most_launched_kernel(tm
     assert gemm["median_us"] == 61.0 and gemm["min_us"] == 60.0
     assert gemm["config"] == {"BLOCK_M": 128, "BLOCK_N": 256}
     assert bp.is_marker(MARK) and not bp.is_marker(FILL)
+    assert not bp.is_marker(MARK.replace("signed char", "unsigned char"))  # torch's uint8 fills
 
 
 def test_a_marks_file_from_another_run_is_refused(tmp_path):
@@ -162,8 +163,8 @@ def test_committed_profiles_describe_the_packaged_configuration_and_this_build()
     configurations dispatch picks today; changing a packaged winner nulls the
     entry (checked on a copy of the packaged table)."""
     from kernelforge import build
-    from kernelforge.kernels import get_operator
-    from kernelforge.runtime.dispatch import select_config
+    from kernelforge.runtime.dispatch import packaged_cache
+    from kernelforge.runtime.env import MI355X_CAPS
     from kernelforge.tuning.config import Problem
 
     bench = _bench()
@@ -172,9 +173,32 @@ def test_committed_profiles_describe_the_packaged_configuration_and_this_build()
     digest = build.source_digest()
     assert doc["library_digest"] == digest
     problem = Problem.create("matmul", "fp16", M=2048, N=4096, K=4096)
-    picked = dict(select_config(get_operator("matmul"), problem, use_packaged=True).config)
+    # What dispatch picks on an MI355X: the packaged winner for the device's key.
+    picked = dict(packaged_cache().get(problem, MI355X_CAPS.key))
     entry, why = bench.profile_entry(path, "gemm_fp16_2048x4096x4096", picked, digest)
     assert why is None, why
     changed = {**picked, "BLOCK_N": 128 if picked["BLOCK_N"] != 128 else 256}
     entry, why = bench.profile_entry(path, "gemm_fp16_2048x4096x4096", changed, digest)
     assert entry is None and "dispatch picked" in why
+
+
+def test_counter_passes_give_per_workload_medians_and_the_derived_clock(tmp_path):
+    """Any other counter pass (MFMA busy, LDS) is summarised the same way; with the
+    kernel-trace durations beside it the table derives the shader clock and the
+    matrix cores' share of busy cycles (2048x4096x4096 recorded on MI355X:
+    29,284,538 busy CU cycles in 66.5 us = 1.72 GHz, 67,108,864 MFMA busy cycles
+    = 57.3%)."""
+    pmc = _counters(tmp_path / "busy.csv", "SQ_BUSY_CU_CYCLES", {GEMM: 29_284_538.0})
+    rows = list(csv.reader(open(pmc)))
+    with open(pmc, "a", newline="") as fh:  # a second counter of the same pass
+        w = csv.writer(fh)
+        for r in rows[1:]:
+            w.writerow(r[:15] + ["SQ_VALU_MFMA_BUSY_CYCLES",
+                                 "67108864.0" if r[8] == GEMM else "0.0"] + r[17:])
+    got = bp.summarize_counters(MARKS, pmc)
+    gemm = got["gemm_fp16_2048x4096x4096"]
+    assert gemm["counters"] == {"SQ_BUSY_CU_CYCLES": 29_284_538.0, "SQ_VALU_MFMA_BUSY_CYCLES": 67_108_864.0}
+    doc = {"commands": ["rocprofv3 --pmc ..."], "library_digest": "x", "kernels": got}
+    md = bp.counters_markdown(doc, {"gemm_fp16_2048x4096x4096": 66.5})
+    line = next(l for l in md.splitlines() if l.startswith("| gemm_fp16"))
+    assert "1.72" in line and "57.3%" in line
