@@ -1,4 +1,4 @@
-// Direct-to-LDS MFMA GEMM for 16-bit inputs on gfx950 (the fast path).
+// Direct-to-LDS MFMA GEMM for 16-bit and fp32 inputs on gfx950 (the fast path).
 //
 // Differences from the register-staged kernel in gemm_impl.h:
 //   * Global -> LDS with global_load_lds_dwordx4: each lane's 16 bytes land at
@@ -27,11 +27,19 @@
 //     32-wide k step with the MFMAs of its first, so LDS latency is spent
 //     under MFMAs and the reads are done by the slice's barrier.
 //
-// Requirements (checked on the host): 16-bit dtype, A k-contiguous with a
-// 16-byte aligned base and row pitch, B either n-contiguous (BLAYOUT 0) or
-// k-contiguous (BLAYOUT 1) with the same alignment, N (BLAYOUT 0) and K
-// multiples of 8, and per-lane byte offsets (BM rows of A, 64 k-rows or BN
-// rows of B) below 4 GiB. BK is 64: one A row of a k-slice is 128 bytes.
+// fp32 runs the same pipeline: a k-slice is 32 elements, so every row of it
+// is still 128 bytes and the A side (DMA, k swizzle, 16-byte fragment reads)
+// is byte for byte the 16-bit one. Each 16x16 fragment step is four
+// v_mfma_f32_16x16x4_f32 over 16 k; n-contiguous B, which has no transposing
+// read for 32-bit elements, is read four bytes per lane per MFMA under its
+// own swizzle (swz_n4).
+//
+// Requirements (checked on the host): 16-bit or fp32 dtype, A k-contiguous
+// with a 16-byte aligned base and row pitch, B either n-contiguous (BLAYOUT
+// 0) or k-contiguous (BLAYOUT 1) with the same alignment, N (BLAYOUT 0) and
+// K multiples of a 16-byte chunk (8 or 4 elements), and per-lane byte
+// offsets (BM rows of A, BK k-rows or BN rows of B) below 4 GiB. BK is 128
+// bytes of elements: one A row of a k-slice is 128 bytes.
 // M/N edges clamp rows/columns (results discarded); the partial last k-slice
 // clamps k into range and zeroes its chunks past K after the DMA lands.
 //
@@ -64,7 +72,9 @@ namespace gemm {
 typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __bf16 bf16x4_t __attribute__((__vector_size__(4 * sizeof(__bf16))));
 
-constexpr int kDirectBK = 64;
+// Every operand row of a k-slice is 128 bytes: 64 elements of a 16-bit type,
+// 32 of fp32.
+constexpr int kSliceRowBytes = 128;
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -183,10 +193,28 @@ __device__ __forceinline__ int swz_n(int chunk, int row) {
   if constexpr (ROW_CHUNKS >= 16) return chunk ^ (((row & 3) << 2) ^ (((row >> 3) & 1) << 1));
   return chunk ^ ((row & 3) << 1);
 }
+// n-contiguous fp32 B rows. Its fragments are read 4 bytes per lane: for one
+// MFMA, lane group g reads 16 columns (64 bytes) of k-row 4g + e, so the four
+// groups read rows 4 apart, whose rows (a multiple of 256 bytes long) fall on
+// the same banks unswizzled. XOR-ing the chunk with row bits 2..3 puts the
+// groups' 64-byte runs in four different quarters of the 256-byte bank
+// window; rows differing in bits 0, 1 and 4 (the MFMAs of a step, the two
+// steps of a slice) share the swizzle, so their offsets differ by immediates.
+template <int ROW_CHUNKS>
+__device__ __forceinline__ int swz_n4(int chunk, int row) {
+  static_assert(ROW_CHUNKS >= 16, "fp32 n-contiguous B needs 16 or more chunks per row");
+  return chunk ^ (((row >> 2) & 3) << 2);
+}
+template <int ES, int ROW_CHUNKS>
+__device__ __forceinline__ int swz_nb(int chunk, int row) {
+  if constexpr (ES == 4) return swz_n4<ROW_CHUNKS>(chunk, row);
+  else return swz_n<ROW_CHUNKS>(chunk, row);
+}
 
-template <int BM, int BN, int WAVES, int STAGES>
+template <int BM, int BN, int WAVES, int STAGES, int ES = 2>
 struct DirectTile {
-  static constexpr int BK = kDirectBK;
+  static constexpr int V = 16 / ES;                   // elements per 16-byte chunk
+  static constexpr int BK = kSliceRowBytes / ES;      // elements per k-slice
   static constexpr int NT = WAVES * kWave;
   static constexpr int WM = WaveGrid<WAVES, BM, BN>::WM;
   static constexpr int WN = WaveGrid<WAVES, BM, BN>::WN;
@@ -195,26 +223,29 @@ struct DirectTile {
   // Fragment edge: 32x32x16 MFMAs for the 256x256 tile, whose 64x128 wave
   // tiles hold 128 accumulators per lane either way but need half the
   // fragment registers of 16x16 pieces; 16x16x32 everywhere else.
-  static constexpr int MF = (BM == 256 && BN == 256) ? 32 : 16;
+  static constexpr int MF = (BM == 256 && BN == 256 && ES == 2) ? 32 : 16;
   static constexpr int FM = TM / MF;
   static constexpr int FN = TN / MF;
-  static constexpr int kSteps = kDirectBK / (MF == 32 ? 16 : 32);  // MFMA k steps per slice
+  // MFMA k steps per slice: 64 bytes of a row each for 16x16 fragments (32
+  // 16-bit k, or 16 fp32 k as four 16x16x4 MFMAs), 32 bytes for 32x32x16.
+  static constexpr int kSteps = MF == 32 ? 4 : 2;
   // Byte sizes of one stage.
-  static constexpr int kABytes = BM * BK * 2;
-  static constexpr int kBBytes = BN * BK * 2;
+  static constexpr int kABytes = BM * kSliceRowBytes;
+  static constexpr int kBBytes = BN * kSliceRowBytes;
   static constexpr int kStageBytes = kABytes + kBBytes;
   // Static LDS: the stages, or the staged C tile of the 32x32 path if larger.
-  static constexpr int kCStageBytes = BM * (BN + 8) * 2;
+  static constexpr int kCStageBytes = BM * (BN + 8) * ES;
   static constexpr int kLdsBytes = (MF == 32 && kCStageBytes > STAGES * kStageBytes)
                                        ? kCStageBytes
                                        : STAGES * kStageBytes;
   // 16-byte chunks per stage and DMA instructions per lane.
-  static constexpr int kAIters = BM * BK / 8 / NT;
-  static constexpr int kBIters = BN * BK / 8 / NT;
+  static constexpr int kAIters = BM * (kSliceRowBytes / 16) / NT;
+  static constexpr int kBIters = BN * (kSliceRowBytes / 16) / NT;
   static constexpr int kPer = kAIters + kBIters;  // vector-memory instructions per slice
-  static constexpr int kBRowChunks = BN / 8;      // BLAYOUT 0: chunks per k-row of B
+  static constexpr int kBRowChunks = BN / V;      // BLAYOUT 0: chunks per k-row of B
   static_assert(STAGES == 2 || STAGES == 3, "two or three LDS stages");
-  static_assert((BM * BK / 8) % NT == 0 && (BN * BK / 8) % NT == 0, "DMA must tile the stage");
+  static_assert((BM * 8) % NT == 0 && (BN * 8) % NT == 0, "DMA must tile the stage");
+  static_assert(ES == 2 || ES == 4, "16-bit or fp32 operands");
   static_assert(TM % MF == 0 && TN % MF == 0, "wave tile must be whole MFMA fragments");
   static_assert(MF == 16 || STAGES == 2, "the 256x256 tile runs two stages");
   static_assert(2 * kPer < 64, "outstanding DMA must fit the vmcnt counter");
@@ -222,7 +253,9 @@ struct DirectTile {
 
 template <typename T, int BM, int BN, int WAVES, int BLAYOUT, int STAGES>
 __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
-  using Tl = DirectTile<BM, BN, WAVES, STAGES>;
+  using Tl = DirectTile<BM, BN, WAVES, STAGES, static_cast<int>(sizeof(T))>;
+  constexpr int ES = static_cast<int>(sizeof(T));  // bytes per element
+  constexpr int V = Tl::V;                         // elements per 16-byte chunk
   constexpr int BK = Tl::BK;
   constexpr int NT = Tl::NT;
   constexpr int FM = Tl::FM, FN = Tl::FN;
@@ -298,11 +331,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   // Chunk q = j*NT + tid is written to LDS slot q; its source is the chunk at
   // the slot's position XOR the row's swizzle. Rows past M (and columns or
   // rows of B past N) are clamped to the last valid one.
-  const char* const a_tile = static_cast<const char*>(args.A) + m0 * args.lda_m * 2 + kt0 * BK * 2;
-  const int64_t lda_b = args.lda_m * 2;
-  const int64_t ldb_b = (BLAYOUT == 0 ? args.ldb_k : args.ldb_n) * 2;  // bytes per B row
+  const char* const a_tile = static_cast<const char*>(args.A) + m0 * args.lda_m * ES + kt0 * BK * ES;
+  const int64_t lda_b = args.lda_m * ES;
+  const int64_t ldb_b = (BLAYOUT == 0 ? args.ldb_k : args.ldb_n) * ES;  // bytes per B row
   const char* const b_tile = static_cast<const char*>(args.B) +
-                             (BLAYOUT == 0 ? n0 * 2 + kt0 * BK * ldb_b : n0 * ldb_b + kt0 * BK * 2);
+                             (BLAYOUT == 0 ? n0 * ES + kt0 * BK * ldb_b : n0 * ldb_b + kt0 * BK * ES);
   // The 256x256 tile computes its per-lane offsets from an opaque copy of the
   // lane id, so the compiler cannot hoist the 64-bit row products out of the
   // segment loop, where they would not fit its registers and spill.
@@ -313,13 +346,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   // swz_k reads row bits 1..3, so the row step must be a multiple of 16.
   static_assert(kRowsPerIter % 16 == 0, "the DMA row step (lanes / 8) must keep the k swizzle: two or more waves");
   const int kr = dtid >> 3;             // this lane's row within an instruction's rows
-  const int kc = swz_k(dtid & 7, kr) * 8;  // its k within the slice; same for every j
+  const int kc = swz_k(dtid & 7, kr) * V;  // its k within the slice; same for every j
   uint32_t a_off[Tl::kAIters];
 #pragma unroll
   for (int j = 0; j < Tl::kAIters; ++j) {
     int64_t r = j * kRowsPerIter + kr;
     r = (m0 + r < M) ? r : (M - 1 - m0);
-    a_off[j] = static_cast<uint32_t>(r * lda_b + kc * 2);
+    a_off[j] = static_cast<uint32_t>(r * lda_b + kc * ES);
   }
   uint32_t b_off[Tl::kBIters];
   // BLAYOUT 0: k-row of chunk j within the slice. Recomputed where the
@@ -330,13 +363,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
     const int q = j * NT + dtid;
     if constexpr (BLAYOUT == 0) {
       const int r = q / Tl::kBRowChunks;
-      int64_t col = swz_n<Tl::kBRowChunks>(q % Tl::kBRowChunks, r) * 8;
-      col = (n0 + col < N) ? col : (N - 8 - n0);
-      b_off[j] = static_cast<uint32_t>(r * ldb_b + col * 2);
+      int64_t col = swz_nb<ES, Tl::kBRowChunks>(q % Tl::kBRowChunks, r) * V;
+      col = (n0 + col < N) ? col : (N - V - n0);
+      b_off[j] = static_cast<uint32_t>(r * ldb_b + col * ES);
     } else {
       int64_t r = j * kRowsPerIter + kr;
       r = (n0 + r < N) ? r : (N - 1 - n0);
-      b_off[j] = static_cast<uint32_t>(r * ldb_b + kc * 2);
+      b_off[j] = static_cast<uint32_t>(r * ldb_b + kc * ES);
     }
   }
   const uint32_t lds_lane0 = static_cast<uint32_t>(wave * 64 * 16);
@@ -347,25 +380,25 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   // Enqueue the DMA of k-slice kt into `stage`.
   auto issue_full = [&](const char* stage, int64_t kt) {
     const uint32_t la = lds_offset(stage) + lds_lane0;
-    const char* ab = a_tile + kt * BK * 2;
-    const char* bb = b_tile + (BLAYOUT == 0 ? kt * BK * ldb_b : kt * BK * 2);
+    const char* ab = a_tile + kt * BK * ES;
+    const char* bb = b_tile + (BLAYOUT == 0 ? kt * BK * ldb_b : kt * BK * ES);
 #pragma unroll
     for (int j = 0; j < Tl::kAIters; ++j) dma16(ab, a_off[j], la + j * NT * 16);
 #pragma unroll
     for (int j = 0; j < Tl::kBIters; ++j) dma16(bb, b_off[j], la + Tl::kABytes + j * NT * 16);
   };
   // The partial last slice: k is clamped into range per lane so every source
-  // stays inside its operand (K % 8 == 0, so K - 8 >= k0); the chunks past K
-  // are zeroed by zero_tail() once the DMA has landed.
-  // Offsets within the slice are 32-bit: `rem` (1..63, a multiple of 8) is
+  // stays inside its operand (K % V == 0, so K - V >= k0); the chunks past K
+  // are zeroed by fix() once the DMA has landed.
+  // Offsets within the slice are 32-bit: `rem` (1..BK-1, a multiple of V) is
   // the number of valid k of the partial slice.
   auto issue_last = [&](const char* stage, int64_t kt) {
     const uint32_t la = lds_offset(stage) + lds_lane0;
     const int64_t k0 = kt * BK;
     const int rem = static_cast<int>(K - k0);
-    const int k = kc < rem ? kc : rem - 8;
-    const uint32_t dk = static_cast<uint32_t>(k * 2) - static_cast<uint32_t>(kc * 2);
-    const char* ab = a_tile + k0 * 2;
+    const int k = kc < rem ? kc : rem - V;
+    const uint32_t dk = static_cast<uint32_t>(k * ES) - static_cast<uint32_t>(kc * ES);
+    const char* ab = a_tile + k0 * ES;
 #pragma unroll
     for (int j = 0; j < Tl::kAIters; ++j) dma16(ab, a_off[j] + dk, la + j * NT * 16);
     if constexpr (BLAYOUT == 0) {
@@ -378,7 +411,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
         dma16(bb, off, la + Tl::kABytes + j * NT * 16);
       }
     } else {
-      const char* bb = b_tile + k0 * 2;
+      const char* bb = b_tile + k0 * ES;
 #pragma unroll
       for (int j = 0; j < Tl::kBIters; ++j) dma16(bb, b_off[j] + dk, la + Tl::kABytes + j * NT * 16);
     }
@@ -436,7 +469,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
     a_frag[c] = ar * 128 + swz_k(kch, ar) * 16;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      if constexpr (BLAYOUT == 0) {
+      if constexpr (BLAYOUT == 0 && ES == 4) {
+        // fp32: lane (g, li) holds column li of k-rows 16c + 4g + e for the
+        // step's four 16x16x4 MFMAs e = 0..3 -- the k of its A chunk 4c + g,
+        // element e. Four 4-byte reads, the rows e apart (same swizzle).
+        const int col = wn * Tl::TN + j * 16 + li;
+        const int r0 = c * 16 + 4 * g;
+        b_frag[c][j] = Tl::kABytes + r0 * (BN * 4) + swz_n4<Tl::kBRowChunks>(col >> 2, r0) * 16 + (col & 3) * 4;
+      } else if constexpr (BLAYOUT == 0) {
         // Transposing reads: a 16-lane group covers 16 columns and 4 k-rows
         // per read; 32x32x16 groups alternate column halves, then k halves.
         const int col = MF == 32 ? wn * Tl::TN + j * 32 + 16 * (g & 1) + (li & 3) * 4
@@ -464,7 +504,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
     for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const u32x4*>(S + a_frag[c] + i * MF * 128);
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      if constexpr (BLAYOUT == 0) {
+      if constexpr (BLAYOUT == 0 && ES == 4) {
+        const char* p = S + bfrag_off(c, j);
+        bf[j] = u32x4{*reinterpret_cast<const uint32_t*>(p),
+                      *reinterpret_cast<const uint32_t*>(p + BN * 4),
+                      *reinterpret_cast<const uint32_t*>(p + 2 * BN * 4),
+                      *reinterpret_cast<const uint32_t*>(p + 3 * BN * 4)};
+      } else if constexpr (BLAYOUT == 0) {
         const uint64_t lo = ds_read_tr4<T>(S + bfrag_off(c, j));
         const uint64_t hi = ds_read_tr4<T>(S + bfrag_off(c, j) + 4 * BN * 2);
         bf[j] = u32x4{static_cast<uint32_t>(lo), static_cast<uint32_t>(lo >> 32),
@@ -494,8 +540,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   // the barrier with most MFMAs still to issue. (Carrying step 1's MFMAs
   // over the barrier instead measured slower: it keeps a third fragment set
   // live.)
-  constexpr int kReads = FM + (BLAYOUT == 0 ? 2 : 1) * FN;  // LDS reads per k step
-  constexpr int kMfma = FM * FN;                           // MFMAs per k step
+  // LDS reads per k step: an A fragment is one 16-byte read; a B fragment one
+  // (k-contiguous), two transposing (16-bit n-contiguous) or four 4-byte reads
+  // (fp32 n-contiguous). MFMA instructions per k step: fp32 fragments take
+  // four 16x16x4 MFMAs each.
+  constexpr int kBReads = BLAYOUT == 1 ? 1 : (ES == 4 ? 4 : 2);
+  constexpr int kReads = FM + kBReads * FN;
+  constexpr int kMfma = FM * FN * (ES == 4 ? 4 : 1);
   constexpr int kPairs = kReads < kMfma ? kReads : kMfma;
   // The 32x32x16 tile runs four 16-wide k steps per slice the same way:
   // step s+1's reads alternate with step s's MFMAs.
@@ -706,9 +757,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
   // outputs (flushed event medians): 2048x4096x4096 at 256x128 68.8 against
   // 70.6 us, 4096x11008x4096 unsplit 360.7 against 371.4 us, 2048x11008x4096
   // 187.8 against 190.9 us; level at 128x256 on 2048x4096x4096.
-  constexpr int kPitch = BN + 8;  // elements per LDS row of the staged C: 16 bytes of padding
-  constexpr bool kCFits = BM * kPitch * 2 <= Tl::kLdsBytes;
-  const bool stage_c = kCFits && args.ldc_n == 1 && (args.ldc_m * 2) % 16 == 0 &&
+  constexpr int kPitch = BN + V;  // elements per LDS row of the staged C: 16 bytes of padding
+  constexpr bool kCFits = BM * kPitch * ES <= Tl::kLdsBytes;
+  const bool stage_c = kCFits && args.ldc_n == 1 && (args.ldc_m * ES) % 16 == 0 &&
                        (reinterpret_cast<uintptr_t>(C) & 15u) == 0;
   if (stage_c) {
     T* const ct = reinterpret_cast<T*>(lds);
@@ -727,17 +778,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
         }
     }
     __syncthreads();
-    constexpr int kRowChunks = BN / 8;
+    constexpr int kRowChunks = BN / V;
     for (int idx = etid; idx < BM * kRowChunks; idx += NT) {
-      const int rl = idx / kRowChunks, cl = (idx % kRowChunks) * 8;
+      const int rl = idx / kRowChunks, cl = (idx % kRowChunks) * V;
       const int64_t row = em0 + rl, col = en0 + cl;
       if (row >= M || col >= N) continue;
       const T* src = ct + rl * kPitch + cl;
       T* dst = C + row * args.ldc_m + col;
-      if (col + 8 <= N) {
+      if (col + V <= N) {
         __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(src), reinterpret_cast<u32x4*>(dst));
       } else {
-        for (int e = 0; e < 8 && col + e < N; ++e) dst[e] = src[e];
+        for (int e = 0; e < V && col + e < N; ++e) dst[e] = src[e];
       }
     }
     __syncthreads();  // the next segment's DMA reuses the stage buffers

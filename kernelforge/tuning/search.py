@@ -43,7 +43,7 @@ DEFAULT_MAX_CANDIDATES = 48
 MFMA_TILE = 16
 
 
-def mfma_fragment_edge(block_m: int, block_n: int, *, direct: int = 0) -> int:
+def mfma_fragment_edge(block_m: int, block_n: int, *, direct: int = 0, elem: int = 2) -> int:
     """Edge of the MFMA output fragments a tile is built from (gemm_direct.h DirectTile::MF).
 
     The direct pipeline's 256x256 tile multiplies with v_mfma_f32_32x32x16:
@@ -51,7 +51,7 @@ def mfma_fragment_edge(block_m: int, block_n: int, *, direct: int = 0) -> int:
     but 32x32 fragments take half the fragment registers. Every other tile
     uses 16x16 fragments.
     """
-    return 32 if direct and block_m == 256 and block_n == 256 else MFMA_TILE
+    return 32 if direct and elem == 2 and block_m == 256 and block_n == 256 else MFMA_TILE
 
 #: k consumed per MFMA step per fragment: 4 lane groups x 16 bytes of operand.
 MFMA_K = {2: 32, 4: 16}
@@ -250,19 +250,27 @@ def gemm_tile_regs(
     lanes = waves * 64
     wm, wn = wave_grid(waves, block_m, block_n)
     acc = block_m * block_n // lanes
-    edge = mfma_fragment_edge(block_m, block_n, direct=direct)
+    edge = mfma_fragment_edge(block_m, block_n, direct=direct, elem=elem)
     frags = 4 * (block_m // wm // edge + block_n // wn // edge) * (2 if direct else 1)
     staged = 0 if direct else 4 * ceil_div((block_m + block_n) * block_k * elem, VECTOR_BYTES * lanes)
     return {"acc": acc, "frags": frags, "staged": staged, "total": acc + frags + staged}
 
 
-#: The direct-to-LDS pipeline moves one 128-byte A row segment per k-slice.
-DIRECT_BLOCK_K = 64
+#: The direct-to-LDS pipeline moves one 128-byte row segment of each operand
+#: row per k-slice.
+DIRECT_ROW_BYTES = 128
+#: Its BLOCK_K for 16-bit inputs (fp32: direct_block_k(4) = 32).
+DIRECT_BLOCK_K = DIRECT_ROW_BYTES // 2
+
+
+def direct_block_k(elem: int) -> int:
+    """Elements of a direct k-slice: one 128-byte row segment."""
+    return DIRECT_ROW_BYTES // elem
 
 
 def gemm_direct_lds_bytes(block_m: int, block_n: int, stages: int) -> int:
-    """LDS of the direct pipeline: dense (unpadded, swizzled) 16-bit stages."""
-    return stages * (block_m + block_n) * DIRECT_BLOCK_K * 2
+    """LDS of the direct pipeline: dense (unpadded, swizzled) stages of 128-byte rows."""
+    return stages * (block_m + block_n) * DIRECT_ROW_BYTES
 
 
 def gemm_direct_static_lds_bytes(block_m: int, block_n: int, stages: int) -> int:
@@ -281,12 +289,19 @@ def gemm_direct_reason(
     block_m: int, block_n: int, block_k: int, waves: int, stages: int, elem: int, caps: DeviceCaps
 ) -> str | None:
     """Extra shape-independent rules of the direct (global->LDS DMA) pipeline."""
-    if elem != 2:
-        return "direct DMA: 16-bit inputs only (the transposing LDS read is b16)"
-    if block_k != DIRECT_BLOCK_K:
-        return f"direct DMA: BLOCK_K must be {DIRECT_BLOCK_K} (one 128-byte A row per slice)"
+    if block_k != direct_block_k(elem):
+        return (f"direct DMA: BLOCK_K must be {direct_block_k(elem)} for {elem}-byte inputs "
+                "(one 128-byte row segment per slice)")
+    if elem == 4 and block_m == 256 and block_n == 256:
+        return "direct DMA: the 256x256 tile multiplies with 16-bit 32x32x16 MFMAs only"
     lanes = waves * 64
-    if (block_m * DIRECT_BLOCK_K // 8) % lanes or (block_n * DIRECT_BLOCK_K // 8) % lanes:
+    if elem == 4 and block_m * block_n // lanes > 64:
+        # Measured: the 4-wave 128x256 and 256x128 fp32 tiles spill 8-160 bytes
+        # per lane (a B fragment is four 4-byte reads, each its own address).
+        return (f"direct DMA: {block_m * block_n // lanes} fp32 accumulators per lane leave no "
+                "registers for the fp32 fragment reads")
+    chunks = DIRECT_ROW_BYTES // VECTOR_BYTES  # 16-byte chunks per row
+    if (block_m * chunks) % lanes or (block_n * chunks) % lanes:
         return f"direct DMA: {block_m}x{block_n} slices do not split into whole 16-byte chunks per lane"
     if block_n < 64:
         return f"direct DMA: BLOCK_N={block_n} leaves too few chunks per row for the bank swizzle"
@@ -407,7 +422,7 @@ class _GemmSpace(SearchSpace):
                 self.operation,
                 BLOCK_M=bm,
                 BLOCK_N=bn,
-                BLOCK_K=64,
+                BLOCK_K=direct_block_k(itemsize(problem.dtype)),
                 GROUP_M=gemm_group_m(bm, bn),
                 DIRECT=1,
                 SPLIT_K=split,

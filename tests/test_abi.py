@@ -94,7 +94,9 @@ def test_variant_table_equals_the_instantiation_rules(lib):
     bm, bn, bk, w, s = staged[2][0]
     assert lib.kf_gemm_has_variant(1, bm, bn, bk, w, s, 0) == 1
     assert lib.kf_gemm_has_variant(1, 48, 48, 32, 4, 2, 0) == 0
-    assert lib.kf_gemm_has_variant(0, 256, 128, 64, 8, 2, 1) == 0  # no fp32 direct pipeline
+    assert lib.kf_gemm_has_variant(0, 256, 128, 64, 8, 2, 1) == 0  # fp32 direct slices are 32 wide
+    assert lib.kf_gemm_has_variant(0, 256, 128, 32, 8, 2, 1) == 1
+    assert lib.kf_gemm_has_variant(0, 256, 256, 32, 8, 2, 1) == 0  # 32x32x16 is 16-bit only
 
 
 def test_workspace_sizing(lib):

@@ -202,6 +202,73 @@ def test_matmul_tiles_and_layouts(tile, layout, m, n, k, dtype):
     _gate(ops.matmul_ref(a, b), out, dtype, f"{cfg} {layout} {m}x{n}x{k}")
 
 
+# fp32 on the DMA pipeline: BLOCK_K = 32 (128-byte rows), four 16x16x4 MFMAs
+# per fragment step, 4-byte reads of n-contiguous B under its own swizzle.
+_FP32_DIRECT_TILES = [
+    (64, 64, 32, 4, 1, 3),
+    (128, 64, 32, 4, 1, 3),
+    (128, 128, 32, 8, 1, 3),
+    (128, 128, 32, 4, 1, 2),
+    (256, 128, 32, 8, 1, 2),
+    (64, 256, 32, 8, 1, 3),
+    (32, 128, 32, 4, 1, 3),
+]
+
+
+@pytest.mark.parametrize("tile", _FP32_DIRECT_TILES, ids=lambda t: "x".join(map(str, t)))
+@pytest.mark.parametrize("layout", ("nn", "nt", "tn"))
+@pytest.mark.parametrize("m,n,k", [(257, 516, 132), (300, 520, 136), (64, 64, 4), (200, 264, 456),
+                                   (1023, 1028, 1000), (130, 260, 127)])
+def test_fp32_direct_tiles_and_layouts(tile, layout, m, n, k):
+    """fp32 direct tiles against the oracle at the fp32 gate (1e-5): row-major
+    B (4-byte reads), k-contiguous B, strided A (staged fallback), K tails that
+    are whole 16-byte chunks (zeroed past K after the DMA) and one that is not
+    (K = 127: the staged twin tile)."""
+    from kernelforge.kernels.matmul import matmul
+
+    bm, bn, bk, w, direct, stages = tile
+    a = _randn(m, k, dtype=torch.float32, seed=11)
+    b = _randn(k, n, dtype=torch.float32, seed=12)
+    da, db = a.to(DEV), b.to(DEV)
+    if layout[1] == "t":
+        db = b.t().contiguous().to(DEV).t()
+    if layout[0] == "t":
+        da = a.t().contiguous().to(DEV).t()
+    cfg = KernelConfig("matmul", BLOCK_M=bm, BLOCK_N=bn, BLOCK_K=bk, GROUP_M=8, DIRECT=direct,
+                       num_warps=w, num_stages=stages)
+    out = matmul(da, db, config=cfg)
+    _gate(ops.matmul_ref(a, b), out, torch.float32, f"{cfg} {layout} {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("split", (1, 2, 4))
+@pytest.mark.parametrize("m,n,k", [(257, 520, 1000), (64, 4096, 4096)])
+def test_fp32_direct_fused_linear_and_split_k(split, m, n, k):
+    """The fp32 direct tile with the bias + GELU epilogue, unsplit and split-K
+    (fp32 partial tiles through the workspace), against the oracle at 1e-5."""
+    from kernelforge.kernels.fused_linear import fused_linear_gelu
+
+    x = _randn(m, k, dtype=torch.float32, seed=m)
+    w = _randn(k, n, dtype=torch.float32, seed=n, scale=k**-0.5)
+    bias = _randn(n, dtype=torch.float32, seed=7)
+    extra = {"SPLIT_K": split} if split > 1 else {}
+    cfg = KernelConfig("fused_linear", BLOCK_M=64, BLOCK_N=128, BLOCK_K=32, GROUP_M=4, DIRECT=1,
+                       num_warps=8, num_stages=3, **extra)
+    out = fused_linear_gelu(x.to(DEV), w.to(DEV), bias.to(DEV), config=cfg)
+    _gate(ops.linear_gelu_ref(x, w, bias), out, torch.float32, f"{cfg} {m}x{n}x{k}")
+
+
+def test_fp32_direct_gemm_at_the_baseline_shape():
+    """2048x4096x4096 fp32 on the direct 128x128 tile: the oracle at 1e-5."""
+    from kernelforge.kernels.matmul import matmul
+
+    a = _randn(2048, 4096, dtype=torch.float32, seed=0, scale=4096**-0.5)
+    b = _randn(4096, 4096, dtype=torch.float32, seed=1, scale=4096**-0.5)
+    cfg = KernelConfig("matmul", BLOCK_M=128, BLOCK_N=128, BLOCK_K=32, GROUP_M=8, DIRECT=1,
+                       num_warps=8, num_stages=3)
+    out = matmul(a.to(DEV), b.to(DEV), config=cfg)
+    _gate(ops.matmul_ref(a, b), out, torch.float32, "fp32 direct 2048x4096x4096")
+
+
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16), ids=("fp16", "bf16"))
 def test_matmul_baseline_config(dtype):
     """BASELINE config 3 (fp16) and its bf16 twin: A[2048,4096] @ B[4096,4096], N(0,1)/sqrt(K)."""

@@ -134,7 +134,12 @@ def test_stage_rules():
 
 def test_direct_rules():
     assert gemm_instantiation_reason(256, 128, 64, 8, 2, 2, MI355X_CAPS, direct=1) is None
-    assert "16-bit" in gemm_instantiation_reason(128, 128, 32, 4, 2, 4, MI355X_CAPS, direct=1)
+    # fp32: 32-element slices (128-byte rows); no 256x256 (a 16-bit MFMA shape);
+    # no 128-accumulator tiles (their fragment reads spill).
+    assert gemm_instantiation_reason(128, 128, 32, 4, 2, 4, MI355X_CAPS, direct=1) is None
+    assert "BLOCK_K must be 32" in gemm_instantiation_reason(128, 128, 64, 8, 3, 4, MI355X_CAPS, direct=1)
+    assert "16-bit" in gemm_instantiation_reason(256, 256, 32, 8, 2, 4, MI355X_CAPS, direct=1)
+    assert "accumulators" in gemm_instantiation_reason(128, 256, 32, 4, 3, 4, MI355X_CAPS, direct=1)
     assert "BLOCK_K must be 64" in gemm_instantiation_reason(128, 128, 32, 4, 2, 2, MI355X_CAPS, direct=1)
     assert "swizzle" in gemm_instantiation_reason(128, 32, 64, 4, 2, 2, MI355X_CAPS, direct=1)
 
@@ -332,7 +337,10 @@ def test_instantiation_list_is_the_rule_filtered_grid():
     assert len(staged[2]) == 59 and len(staged[4]) == 80 and len(direct[2]) == 39
     # The one 32x32x16 tile: 256x256 on eight waves, two 64 KiB stages.
     assert [t for t in direct[2] if t[0] == t[1] == 256] == [(256, 256, 64, 8, 2)]
-    assert direct[4] == [] and all(t[2] == 64 for t in direct[2])
+    # fp32 direct tiles: 32-element slices, no 256x256, at most 64 accumulators per lane.
+    assert len(direct[4]) == 34 and all(t[2] == 64 for t in direct[2])
+    assert all(t[2] == 32 and t[0] * t[1] < 256 * 256 and t[0] * t[1] // (64 * t[3]) <= 64
+               for t in direct[4])
     for elem, tiles in staged.items():
         for bm, bn, bk, w, s in tiles:
             assert gemm_instantiation_reason(bm, bn, bk, w, s, elem, MI355X_CAPS) is None
