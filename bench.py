@@ -375,11 +375,11 @@ def main(argv: list[str] | None = None) -> int:
         mean_ms = float(np.mean(flushed))
         rate = (work / (mean_ms * 1e-3)) / scale
         if args.no_sustained:
-            sustained_ms, dev = float("nan"), 0.0
+            sustained_ms, replay_diff = float("nan"), 0.0
         else:
-            sustained_ms, dev = _time_graph(fns, steps, warmup, flush)
-        if dev != 0.0:
-            raise RuntimeError(f"{name}: graph replay differs from the eager result by {dev:.3g}")
+            sustained_ms, replay_diff = _time_graph(fns, steps, warmup, flush)
+        if replay_diff != 0.0:
+            raise RuntimeError(f"{name}: graph replay differs from the eager result by {replay_diff:.3g}")
         entry = {
             "value": rate,
             "unit": unit,

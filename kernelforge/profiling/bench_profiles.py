@@ -22,7 +22,13 @@ kernel dispatch no longer picks (it then reports the kernel figures as null,
 with the reason).
 
     python -m kernelforge.profiling.bench_profiles --marks M.json --trace T.csv \\
-        [--fetch F.csv --write W.csv] --command "..." [--command "..."] --out profiles
+        [--fetch F.csv --write W.csv] [--pmc P.csv ...] [--trace-command "..."] \\
+        [--traffic-command "..."] [--pmc-command "..."] --out profiles
+
+Counter passes other than the traffic pair (``--pmc``, any counters) are
+summarised per workload into ``bench_counters.json``, whose table derives the
+shader clock and the matrix cores' share of busy cycles where the counters
+allow.
 """
 
 from __future__ import annotations

@@ -365,9 +365,9 @@ def run(target: list[str], *, out_dir: str | Path, passes: tuple[str, ...] = DEF
                 notes.append(f"pass '{name}': rocprofv3 exited on SIGSEGV (status {rc}) "
                              + ("before the profiled program finished" if not finished
                                 else "with no measured launch in its output"))
-        if measured is None:
-            if rc == 0:
-                codes[-1] = 1  # ran, but recorded no launch of this library
+        if measured is None and rc == 0:
+            codes[-1] = 1  # ran, but recorded no launch of this library
+        if codes[-1] != 0:
             break  # a failed pass ends the profile: nothing further runs on the GPU
         launch.absorb(measured, timed=not PASSES[name])
         found = True

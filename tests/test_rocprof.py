@@ -241,6 +241,19 @@ def test_a_profiler_segfault_before_the_program_finished_fails_the_profile(monke
     assert "before the profiled program finished" in run.notes[0]
 
 
+def test_a_failed_pass_ends_the_profile_even_when_its_files_hold_the_launch(monkeypatch, tmp_path):
+    """A pass whose status stands as a failure starts no further pass on the GPU,
+    and its counters are not merged into the result."""
+    ran = []
+    _fake_passes(monkeypatch, {"trace": (0, rocprof.CHILD_DONE), "mfma": (-11, "partial"),
+                               "fetch": (0, rocprof.CHILD_DONE)})
+    inner = rocprof._run_pass
+    monkeypatch.setattr(rocprof, "_run_pass", lambda c, t: (ran.append(c[c.index("-o") + 1]), inner(c, t))[1])
+    run = rocprof.run(["python"], out_dir=tmp_path, passes=("trace", "mfma", "fetch"))
+    assert ran == ["trace", "mfma"] and not run.ok and run.returncodes == [0, -11]
+    assert run.launch is not None and not run.launch.counters
+
+
 def test_the_launch_once_child_prints_the_completion_line_last():
     """The parent recognises a finished child by this line; it must be what
     _launch_once prints after its measured launch has synchronised."""
