@@ -364,6 +364,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
     if constexpr (BLAYOUT == 0) {
       const int r = q / Tl::kBRowChunks;
       int64_t col = swz_nb<ES, Tl::kBRowChunks>(q % Tl::kBRowChunks, r) * V;
+      // The last whole chunk of the row; N % V == 0 (kf_gemm admits n-contiguous
+      // B on this pipeline only then), so it lies at or right of n0.
       col = (n0 + col < N) ? col : (N - V - n0);
       b_off[j] = static_cast<uint32_t>(r * ldb_b + col * ES);
     } else {
