@@ -522,11 +522,18 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_direct_kernel(Args args) {
       }
     }
   };
+  // Snake order: odd fragment rows walk the columns backwards, so every MFMA
+  // after the first changes one operand, never both. Random operands hold the
+  // board at its power limit and fewer operand changes buy clock: 0.4-0.8%
+  // on 2048x4096x4096 (fp16, bf16) and 0.2-0.3% on the fused 4096x11008x4096,
+  // interleaved flushed medians, bit-identical outputs (each accumulator
+  // keeps its k order).
   auto mma_all = [&](const u32x4 (&af)[FM], const u32x4 (&bf)[FN]) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
+      for (int jj = 0; jj < FN; ++jj) {
+        const int j = (i & 1) ? FN - 1 - jj : jj;
         if constexpr (MF == 32)
           Mma32<T>::run(af[i], bf[j], acc[i][j]);
         else
