@@ -14,7 +14,10 @@ kernel), and writes:
   its configuration, and the mean, median and minimum dispatch duration;
 * ``hbm_traffic.json``: per workload FETCH_SIZE and WRITE_SIZE per dispatch
   (medians) scaled to bytes by what the same counters read for the 1 GiB copy;
-* markdown tables of both, each with the commands that produced it.
+* markdown tables of both, each with the commands that produced it;
+* with ``--stats``, ``bench_kernel_stats.md``: rocprofv3's ``--stats`` table
+  of the kernel-trace run (whole-run average per kernel), the workloads'
+  kernels named.
 
 Both JSON files carry the library's source digest and each workload's
 configuration, so ``bench.py`` can refuse a profile of another build or of a
@@ -22,8 +25,8 @@ kernel dispatch no longer picks (it then reports the kernel figures as null,
 with the reason).
 
     python -m kernelforge.profiling.bench_profiles --marks M.json --trace T.csv \\
-        [--fetch F.csv --write W.csv] [--pmc P.csv ...] [--trace-command "..."] \\
-        [--traffic-command "..."] [--pmc-command "..."] --out profiles
+        [--stats S.csv] [--fetch F.csv --write W.csv] [--pmc P.csv ...] \\
+        [--trace-command "..."] [--traffic-command "..."] [--pmc-command "..."] --out profiles
 
 Counter passes other than the traffic pair (``--pmc``, any counters) are
 summarised per workload into ``bench_counters.json``, whose table derives the
@@ -34,6 +37,7 @@ allow.
 from __future__ import annotations
 
 import argparse
+import csv
 import json
 import statistics
 from collections import Counter
@@ -204,6 +208,52 @@ CU over the median kernel-trace duration (kernel_trace.json, a separate run of t
 """ + "\n".join(rows) + "\n"
 
 
+def summarize_stats(stats_csv: str | Path, traced: dict | None = None, top: int = 12) -> list[dict]:
+    """rocprofv3's ``--stats`` table (``*_kernel_stats.csv``: one row per kernel
+    name over the whole run): every workload's kernel and the ``top`` kernels by
+    total time, in order of total time. A kernel that is some workload's kernel
+    in ``traced`` (kernel_trace.json's entries) is named by that workload, so its
+    whole-run average can be set beside the per-workload median."""
+    by_kernel: dict[str, list[str]] = {}
+    for name, e in (traced or {}).items():
+        by_kernel.setdefault(e["kernel"], []).append(name)
+    rows = []
+    with open(stats_csv, newline="") as handle:
+        for r in csv.DictReader(handle):
+            rows.append({"kernel": r["Name"], "calls": int(r["Calls"]),
+                         "total_us": float(r["TotalDurationNs"]) / 1e3,
+                         "average_us": float(r["AverageNs"]) / 1e3,
+                         "min_us": float(r["MinNs"]) / 1e3, "max_us": float(r["MaxNs"]) / 1e3,
+                         "percent": float(r["Percentage"]),
+                         "workloads": by_kernel.get(r["Name"], [])})
+    rows.sort(key=lambda r: -r["total_us"])
+    return [r for i, r in enumerate(rows) if i < top or r["workloads"]]
+
+
+def stats_markdown(rows: list[dict], commands: list[str], digest: str) -> str:
+    body = "\n".join(
+        f"| `{_short(r['kernel'], 70)}` | {', '.join(r['workloads']) or '-'} | {r['calls']} | "
+        f"{r['average_us']:.1f} | {r['min_us']:.1f} | {r['max_us']:.1f} | {r['percent']:.1f} |"
+        for r in rows)
+    cmds = "\n".join(commands)
+    return f"""# rocprofv3 --stats of the bench workloads run
+
+The `--stats` table of the kernel-trace run (repository root, one MI355X), the kernels with the
+most total time. Averages are over every dispatch of a kernel in the run (correctness
+checks, comparisons, warm-up and timed steps), so they sit beside the per-workload medians
+of `kernel_trace.json`, which count only the workload's own segment.
+
+```
+{cmds}
+```
+
+Library source digest: `{digest}`.
+
+| kernel | workload | calls | average us | min us | max us | % of kernel time |
+|---|---|---|---|---|---|---|
+""" + body + "\n"
+
+
 def _short(name: str, width: int = 90) -> str:
     return name if len(name) <= width else name[: width - 3] + "..."
 
@@ -275,6 +325,7 @@ def main(argv: list[str] | None = None) -> int:
                         "per-workload medians go to bench_counters.json")
     p.add_argument("--pmc-command", action="append", default=[],
                    help="command lines that produced the --pmc passes")
+    p.add_argument("--stats", help="*_kernel_stats.csv of the kernel-trace pass (rocprofv3 --stats)")
     p.add_argument("--out", default="profiles")
     args = p.parse_args(argv)
     marks = load_marks(args.marks)
@@ -289,6 +340,11 @@ def main(argv: list[str] | None = None) -> int:
                "kernels": summarize_trace(marks, args.trace)}
         (out / "kernel_trace.json").write_text(json.dumps(doc, indent=1) + "\n")
         (out / "bench_workloads_kernel_trace.md").write_text(trace_markdown(doc))
+        if args.stats:
+            rows = summarize_stats(args.stats, doc["kernels"])
+            (out / "bench_kernel_stats.md").write_text(
+                stats_markdown(rows, [*args.trace_command, me + f" --stats {args.stats}"],
+                               marks["library_digest"]))
     if args.fetch and args.write:
         doc = {"commands": [*args.traffic_command, me], "library_digest": marks["library_digest"],
                **summarize_traffic(marks, args.fetch, args.write)}

@@ -202,3 +202,23 @@ def test_counter_passes_give_per_workload_medians_and_the_derived_clock(tmp_path
     md = bp.counters_markdown(doc, {"gemm_fp16_2048x4096x4096": 66.5})
     line = next(l for l in md.splitlines() if l.startswith("| gemm_fp16"))
     assert "1.72" in line and "57.3%" in line
+
+
+def test_the_stats_table_names_each_workloads_kernel(tmp_path):
+    """rocprofv3 --stats rows (one per kernel name over the whole run) come out
+    by total time, with the workload whose kernel each one is."""
+    stats = tmp_path / "bench_kernel_stats.csv"
+    with open(stats, "w", newline="") as fh:
+        w = csv.writer(fh)
+        w.writerow(["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage", "MinNs", "MaxNs", "StdDev"])
+        w.writerow([REDUCE, 950, 81_664_163, 85962.3, 27.3, 78_550, 100_827, 5458.3])
+        w.writerow([GEMM, 121, 7_388_284, 61060.2, 2.47, 59_712, 66_071, 1269.2])
+        w.writerow([ROWS, 61, 1_320_000, 21639.3, 0.44, 20_100, 23_000, 500.0])
+    traced = bp.summarize_trace(MARKS, _trace(tmp_path / "t_kernel_trace.csv"))
+    rows = bp.summarize_stats(stats, traced, top=1)  # the top kernel, then the workloads' kernels
+    assert [r["kernel"] for r in rows] == [REDUCE, GEMM, ROWS]
+    assert rows[2]["workloads"] == ["rmsnorm_fp32_4096x4096"]
+    assert rows[1]["workloads"] == ["gemm_fp16_2048x4096x4096"] and rows[0]["workloads"] == []
+    assert rows[1]["average_us"] == pytest.approx(61.0602) and rows[1]["calls"] == 121
+    md = bp.stats_markdown(rows, ["rocprofv3 --kernel-trace --stats ..."], "abc")
+    assert "| gemm_fp16_2048x4096x4096 | 121 | 61.1 |" in md and "rocprofv3 --kernel-trace --stats" in md
